@@ -1,0 +1,133 @@
+/*
+ * mx_paged_decode.h -- C ABI of the MI355X (gfx950) paged GQA decode attention library
+ * (libmxattn.so).
+ *
+ * Operator (reference task.md:138-148): for every sequence b and query head h,
+ *   kv      = h / (num_heads / num_kv_heads)
+ *   tokens  = the first seq_lens[b] tokens of sequence b; token t lives in physical page
+ *             block_table[b, t / page_size] at in-page offset t % page_size
+ *   out[b,h,:] = softmax(q[b,h,:] . K[tokens,kv,:]^T * scale) . V[tokens,kv,:]
+ *
+ * Layouts (all contiguous, row-major):
+ *   q, out       [batch, num_heads, head_dim]            bf16  (== [batch, 1, num_heads, head_dim])
+ *   k/v cache    [num_pages, page_size, num_kv_heads, head_dim]  bf16
+ *   seq_lens     [batch]                                  int32
+ *   block_table  [batch, max_pages_per_seq]               int32
+ * Only the first ceil(seq_lens[b] / page_size) entries of a block_table row are read; the
+ * padding entries after them are never touched (reference task.md:8-10, 61, 92).
+ *
+ * Supported shapes: head_dim in {64, 128, 256}; page_size in {16, 32, 64, 128, 256};
+ * num_heads % num_kv_heads == 0 and num_heads / num_kv_heads <= 16; seqlen_q == 1; causal == 0.
+ *
+ * Every call is asynchronous on the given stream (NULL = the legacy default stream) and never
+ * synchronises.  Calls that share one workspace (including the library's internal one) must
+ * be ordered on one stream.
+ */
+#ifndef MX_PAGED_DECODE_H
+#define MX_PAGED_DECODE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes returned by the int-returning entry points (also kept for mx_last_status()). */
+#define MX_STATUS_OK 0
+#define MX_STATUS_NULL_POINTER (-1)         /* a required pointer is NULL                    */
+#define MX_STATUS_INVALID_SHAPE (-2)        /* sizes inconsistent (e.g. Hq % Hkv != 0)       */
+#define MX_STATUS_UNSUPPORTED (-3)          /* valid but not implemented (D, page size, ...) */
+#define MX_STATUS_WORKSPACE_TOO_SMALL (-4)  /* caller workspace smaller than required        */
+#define MX_STATUS_HIP_ERROR (-5)            /* HIP runtime reported an error                 */
+#define MX_STATUS_ALLOC_FAILED (-6)         /* internal workspace allocation failed          */
+#define MX_STATUS_INVALID_ARGUMENT (-7)     /* bad non-shape argument (phase, scale, ...)    */
+
+/* Bits of the device status word (sticky; read with mx_read_device_status). */
+#define MX_DEVICE_BAD_PAGE_ID 1u    /* a valid block_table slot held an id outside [0, num_pages) */
+#define MX_DEVICE_SEQ_TOO_LONG 2u   /* seq_lens[b] exceeded the capacity the call was planned for */
+
+/* Phase flags for mx_paged_gqa_decode (0 = run everything). */
+#define MX_PHASE_MAIN_ONLY 1        /* run only the split-KV kernel; partials stay in workspace */
+#define MX_PHASE_COMBINE_ONLY 2     /* run only the combine over partials of an identical call  */
+
+/*
+ * Drop-in replacement for the reference's C500 kernel entry point, same name, argument order
+ * and meaning: reference task.md:38-54, implementation submission_clean.cu:432-447, bound by
+ * verify_real.py:12-14 / bench_all.py:98-100 as argtypes [c_void_p]*6 + [c_int64]*9.
+ *   - scale is derived as 1/sqrt(headdim) (submission_clean.cu:451);
+ *   - block_table row width = num_blocks / batch_size (submission_clean.cu:449, task.md:61);
+ *   - seqlen_k is the capacity used for split planning (task.md:7, 131);
+ *   - launches on the legacy default stream, no synchronisation (task.md:67);
+ *   - uses a library-owned, grow-only workspace per device (submission_clean.cu:478-491).
+ * Returns nothing, as the reference does; on invalid arguments nothing is launched, a message
+ * is printed to stderr and the status is kept for mx_last_status() / mx_last_error().
+ */
+void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_paged,
+                void* output, const int32_t* cache_seqlens, const int32_t* block_table,
+                int64_t batch_size, int64_t seqlen_k, int64_t seqlen_q, int64_t num_heads,
+                int64_t num_heads_k, int64_t headdim, int64_t page_block_size,
+                int64_t num_blocks, int64_t causal);
+
+/*
+ * Extended entry point (replaces the same run_kernel, submission_clean.cu:432-504, with an
+ * explicit scale, table width, pool size, split override, workspace and stream, and a status).
+ *   num_pages          pool size; page ids outside [0, num_pages) are flagged and read as page 0.
+ *                      0 = unknown (only negative ids are flagged).
+ *   max_pages_per_seq  block_table row width.
+ *   max_seq_len        capacity the split plan is sized for (<= 0: max_pages_per_seq*page_size).
+ *                      seq_lens[b] beyond the planned capacity (max_seq_len rounded up to whole
+ *                      splits, at most max_pages_per_seq*page_size) are clamped and flagged
+ *                      (MX_DEVICE_SEQ_TOO_LONG).
+ *   num_splits         0 = automatic policy, otherwise the requested split count (clamped to
+ *                      the number of pages of max_seq_len).
+ *   workspace          device memory of >= mx_paged_gqa_decode_workspace_size() bytes,
+ *                      zero-filled once by the caller before first use; NULL = library-owned.
+ *   phase              0, MX_PHASE_MAIN_ONLY or MX_PHASE_COMBINE_ONLY.
+ *   stream             hipStream_t (NULL = legacy default stream).
+ * Returns MX_STATUS_OK or a negative MX_STATUS_* code; nothing is launched on error.
+ */
+int mx_paged_gqa_decode(const void* q, const void* k_cache, const void* v_cache, void* out,
+                        const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
+                        int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                        int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
+                        int64_t max_seq_len, float scale, int64_t num_splits, void* workspace,
+                        int64_t workspace_bytes, int32_t phase, void* stream);
+
+/*
+ * Host-only planning (no HIP call when num_cus > 0): validates the shape and reports the split
+ * count, tokens per split and workspace bytes a call with these arguments would use.  Replaces
+ * the reference's split policy choose_num_splits (submission_clean.cu:375-430) and its
+ * page-rounding of splits (submission_clean.cu:456-461).  num_cus <= 0 queries the current
+ * device.  Any of the out pointers may be NULL.
+ */
+int mx_paged_gqa_decode_plan(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
+                             int64_t head_dim, int64_t page_size, int64_t max_pages_per_seq,
+                             int64_t max_seq_len, int64_t num_splits, int64_t num_cus,
+                             int64_t* splits_out, int64_t* tokens_per_split_out,
+                             int64_t* workspace_bytes_out);
+
+/* Workspace bytes a call needs (replaces the grow-only sizing of submission_clean.cu:463,
+ * 478-491); negative MX_STATUS_* on invalid arguments.  Queries the current device's CU count
+ * when num_splits == 0. */
+int64_t mx_paged_gqa_decode_workspace_size(int64_t batch, int64_t num_heads,
+                                           int64_t num_kv_heads, int64_t head_dim,
+                                           int64_t page_size, int64_t max_pages_per_seq,
+                                           int64_t max_seq_len, int64_t num_splits);
+
+/* Copies the sticky device status word (MX_DEVICE_* bits) of a workspace (NULL = the library's
+ * workspace of the current device) to *flags_out after synchronising the stream; clears it
+ * when reset != 0.  Not part of the reference (which validates nothing on the device). */
+int mx_read_device_status(void* workspace, int32_t reset, void* stream, int32_t* flags_out);
+
+/* Status and message of the last failing call on this host thread (reference has none). */
+int mx_last_status(void);
+const char* mx_last_error(void);
+
+/* Library version string. */
+const char* mx_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MX_PAGED_DECODE_H */

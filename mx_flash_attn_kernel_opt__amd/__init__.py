@@ -1,0 +1,29 @@
+"""MI355X (gfx950) paged GQA decode attention.
+
+The one operator of the reference (task.md:138-148) as a hand-written HIP library,
+libmxattn.so, with the reference's C entry point ``run_kernel`` (task.md:38-54) and an
+extended C ABI (include/mx_paged_decode.h).  This package loads the library with ctypes and
+exposes it over PyTorch-ROCm device tensors; it has no CPU fallback.
+"""
+
+from ._lib import MXAttnError, library_path, load  # noqa: F401
+from .decode import (  # noqa: F401
+    make_workspace,
+    paged_gqa_decode,
+    plan,
+    read_device_status,
+    run_kernel,
+    workspace_size,
+)
+
+__all__ = [
+    "MXAttnError",
+    "library_path",
+    "load",
+    "make_workspace",
+    "paged_gqa_decode",
+    "plan",
+    "read_device_status",
+    "run_kernel",
+    "workspace_size",
+]

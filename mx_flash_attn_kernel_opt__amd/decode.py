@@ -1,0 +1,154 @@
+"""Python face of the paged GQA decode operator.
+
+``run_kernel`` keeps the reference's operator surface: the C500 contest entry point
+``run_kernel`` (reference task.md:38-54), called the way its harness calls it
+(verify_real.py:32-38: device tensors passed by ``data_ptr()``).  ``paged_gqa_decode`` is the
+tensor-level entry of the extended C ABI (explicit scale, split override, workspace, stream).
+Both go straight to libmxattn.so; there is no CPU or PyTorch fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _stream_handle(stream, device: torch.device) -> ctypes.c_void_p:
+    if stream is None:
+        stream = torch.cuda.current_stream(device)
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def plan(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
+         max_pages_per_seq: int, max_seq_len: int = 0, num_splits: int = 0,
+         num_cus: int = 0) -> dict:
+    """Split plan of a call (host only when ``num_cus`` > 0).
+
+    Returns ``{"splits", "tokens_per_split", "workspace_bytes"}``; raises MXAttnError for an
+    invalid or unsupported shape.
+    """
+    lib = _lib.load()
+    ns, tps, ws = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    st = lib.mx_paged_gqa_decode_plan(batch, num_heads, num_kv_heads, head_dim, page_size,
+                                      max_pages_per_seq, max_seq_len, num_splits, num_cus,
+                                      ctypes.byref(ns), ctypes.byref(tps), ctypes.byref(ws))
+    _lib.check(st)
+    return {"splits": ns.value, "tokens_per_split": tps.value, "workspace_bytes": ws.value}
+
+
+def workspace_size(batch: int, num_heads: int, num_kv_heads: int, head_dim: int,
+                   page_size: int, max_pages_per_seq: int, max_seq_len: int = 0,
+                   num_splits: int = 0) -> int:
+    n = _lib.load().mx_paged_gqa_decode_workspace_size(
+        batch, num_heads, num_kv_heads, head_dim, page_size, max_pages_per_seq, max_seq_len,
+        num_splits)
+    if n < 0:
+        _lib.check(int(n))
+    return int(n)
+
+
+def make_workspace(nbytes: int, device) -> torch.Tensor:
+    """Zero-filled device workspace (the status word must start at zero)."""
+    return torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+def paged_gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                     block_table: torch.Tensor, seq_lens: torch.Tensor,
+                     scale: float | None = None, *, out: torch.Tensor | None = None,
+                     num_splits: int = 0, max_seq_len: int = 0,
+                     workspace: torch.Tensor | None = None, phase: int = 0,
+                     stream=None) -> torch.Tensor:
+    """out[b, h] = softmax(q[b, h] . K_b^T * scale) . V_b over the first seq_lens[b] tokens.
+
+    q: [B, Hq, D] or [B, 1, Hq, D] bf16; k_cache / v_cache: [num_pages, page_size, Hkv, D]
+    bf16; block_table: [B, max_pages] int32; seq_lens: [B] int32; all on one GPU, contiguous.
+    ``scale`` defaults to 1/sqrt(D) (reference submission_clean.cu:451).
+    """
+    _require(q.is_cuda, "q must be a device tensor")
+    dev = q.device
+    for name, t, dt in (("q", q, torch.bfloat16), ("k_cache", k_cache, torch.bfloat16),
+                        ("v_cache", v_cache, torch.bfloat16),
+                        ("block_table", block_table, torch.int32),
+                        ("seq_lens", seq_lens, torch.int32)):
+        _require(t.device == dev, f"{name} must be on {dev}")
+        _require(t.dtype == dt, f"{name} must be {dt}, got {t.dtype}")
+        _require(t.is_contiguous(), f"{name} must be contiguous")
+    if q.dim() == 4:
+        _require(q.shape[1] == 1, "only one query token per sequence (seqlen_q == 1)")
+        q3 = q.view(q.shape[0], q.shape[2], q.shape[3])
+    else:
+        _require(q.dim() == 3, "q must be [B, Hq, D] or [B, 1, Hq, D]")
+        q3 = q
+    B, Hq, D = q3.shape
+    _require(k_cache.dim() == 4 and k_cache.shape == v_cache.shape,
+             "k_cache and v_cache must both be [num_pages, page_size, Hkv, D]")
+    num_pages, P, Hkv, Dk = k_cache.shape
+    _require(Dk == D, "head_dim of q and the caches differ")
+    _require(block_table.dim() == 2 and block_table.shape[0] == B,
+             "block_table must be [B, max_pages]")
+    _require(seq_lens.shape == (B,), "seq_lens must be [B]")
+    if out is None:
+        out = torch.empty_like(q)
+    else:
+        _require(out.shape == q.shape and out.dtype == torch.bfloat16 and out.is_contiguous()
+                 and out.device == dev, "out must be a contiguous bf16 tensor shaped like q")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    ws_bytes = 0
+    if workspace is not None:
+        _require(workspace.is_cuda and workspace.device == dev and workspace.is_contiguous(),
+                 "workspace must be a contiguous tensor on the same device")
+        ws_bytes = workspace.numel() * workspace.element_size()
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        st = lib.mx_paged_gqa_decode(
+            _ptr(q3), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(seq_lens),
+            _ptr(block_table), B, Hq, Hkv, D, P, num_pages, block_table.shape[1], max_seq_len,
+            float(scale), num_splits, _ptr(workspace), ws_bytes, phase,
+            _stream_handle(stream, dev))
+    _lib.check(st)
+    return out
+
+
+def run_kernel(q, k_cache_paged, v_cache_paged, output, cache_seqlens, block_table,
+               batch_size, seqlen_k, seqlen_q, num_heads, num_heads_k, headdim,
+               page_block_size, num_blocks, causal) -> None:
+    """The reference's 15-argument entry point (task.md:38-54) over device tensors.
+
+    Exactly what the reference harness does (verify_real.py:32-38): pass ``data_ptr()`` of
+    each tensor and the 9 int64 scalars to the C symbol ``run_kernel`` of libmxattn.so.  Like
+    the reference it returns nothing; an argument error is printed by the library and raised
+    here from ``mx_last_status``.
+    """
+    lib = _lib.load()
+    lib.run_kernel(_ptr(q), _ptr(k_cache_paged), _ptr(v_cache_paged), _ptr(output),
+                   _ptr(cache_seqlens), _ptr(block_table), batch_size, seqlen_k, seqlen_q,
+                   num_heads, num_heads_k, headdim, page_block_size, num_blocks, causal)
+    _lib.check(lib.mx_last_status())
+
+
+def read_device_status(workspace: torch.Tensor | None = None, reset: bool = True,
+                       stream=None, device=None) -> int:
+    """Sticky MX_DEVICE_* bits raised by the kernels (synchronises the stream)."""
+    lib = _lib.load()
+    dev = workspace.device if workspace is not None else torch.device(
+        device if device is not None else "cuda")
+    flags = ctypes.c_int32()
+    with torch.cuda.device(dev):
+        st = lib.mx_read_device_status(_ptr(workspace), int(bool(reset)),
+                                       _stream_handle(stream, dev), ctypes.byref(flags))
+    _lib.check(st)
+    return int(flags.value)

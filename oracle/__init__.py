@@ -1,0 +1,31 @@
+"""TEST INFRASTRUCTURE ONLY: the CPU oracle (checker) of the paged GQA decode operator.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import this package, and only to check or to time the CPU baseline.  The product path
+(``mx_flash_attn_kernel_opt__amd``) never imports it and has no CPU fallback.
+
+Pinning (what each function is checked against, in tests/test_oracle.py):
+  paged_decode_reference  fp32 torch restatement of task.md:138-148.  Pinned by the fp64
+                          brute force below, by torch's own scaled_dot_product_attention on
+                          contiguous layouts (an independent library routine), by closed-form
+                          known answers (L=1 -> the V row, constant V, q=0 -> mean of V,
+                          identical K rows -> mean of V) and by invariants (page permutation,
+                          poisoned padding, KV-head permutation).
+  paged_decode_fp64       fp64 numpy brute force over tokens (small shapes only); pinned by the
+                          same known answers.
+  split_partials / combine_partials
+                          the split-KV + log-sum-exp merge (optimized_c500_flash_attn.cu:537-551,
+                          666-728); pinned by equality with the unsplit oracle for every split
+                          size.
+No reference-held fixtures exist for this path (the reference checks live against the absent
+third-party flash_attn_with_kvcache, verify_real.py:40-41), so parity with that library is
+unpinned; the task.md:85-96 example is kept as a shape fixture under tests/golden/.
+"""
+
+from .paged_attention import (  # noqa: F401
+    combine_partials,
+    kv_bytes,
+    paged_decode_fp64,
+    paged_decode_reference,
+    split_partials,
+)
