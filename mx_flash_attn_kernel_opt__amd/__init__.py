@@ -8,6 +8,7 @@ exposes it over PyTorch-ROCm device tensors; it has no CPU fallback.
 
 from ._lib import MXAttnError, library_path, load  # noqa: F401
 from .decode import (  # noqa: F401
+    BoundDecode,
     make_workspace,
     paged_gqa_decode,
     plan,
@@ -17,6 +18,7 @@ from .decode import (  # noqa: F401
 )
 
 __all__ = [
+    "BoundDecode",
     "MXAttnError",
     "library_path",
     "load",

@@ -83,13 +83,45 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
 }
 
-// 16-byte / 8-byte loads at a wave-uniform base plus a per-lane unsigned byte offset, the
-// form the backend maps to global_load with an SGPR base and a 32-bit VGPR offset.
-__device__ __forceinline__ u32x4 ld16(const uint16_t* base, uint32_t byte_off) {
-  return *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + byte_off);
+
+// Register image of one 16-token chunk of one KV head.
+//   k[i]    : K[token r16][32*i + 8*g4 .. +7]            (A operand of QK MFMA i)
+//   v[r][w] : V[token 4*g4 + r][(D/16)*r16 + 2w .. +1]   (D/32 dwords per row)
+// Compile-time tuning knobs (defaults are the measured best on MI355X).
+#ifndef MX_NBUF_D64
+#define MX_NBUF_D64 2
+#endif
+#ifndef MX_NBUF_D128
+#define MX_NBUF_D128 2
+#endif
+#ifndef MX_NBUF_D256
+#define MX_NBUF_D256 2
+#endif
+#ifndef MX_KV_NONTEMPORAL
+#define MX_KV_NONTEMPORAL 0
+#endif
+
+template <int D>
+constexpr int ring_depth() {
+  return D == 64 ? MX_NBUF_D64 : (D == 128 ? MX_NBUF_D128 : MX_NBUF_D256);
 }
-__device__ __forceinline__ u32x2 ld8(const uint16_t* base, uint32_t byte_off) {
-  return *reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(base) + byte_off);
+
+// K/V stream loads: wave-uniform base plus per-lane byte offset.
+__device__ __forceinline__ u32x4 ld_kv16(const uint16_t* base, uint32_t byte_off) {
+  const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + byte_off);
+#if MX_KV_NONTEMPORAL
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
+}
+__device__ __forceinline__ u32x2 ld_kv8(const uint16_t* base, uint32_t byte_off) {
+  const u32x2* p = reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(base) + byte_off);
+#if MX_KV_NONTEMPORAL
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
 }
 
 // Register image of one 16-token chunk of one KV head.
@@ -105,13 +137,13 @@ template <int D>
 __device__ __forceinline__ void load_v_row(uint32_t (&dst)[D / 32], const uint16_t* base,
                                            uint32_t byte_off) {
   if constexpr (D == 64) {
-    const u32x2 x = ld8(base, byte_off);
+    const u32x2 x = ld_kv8(base, byte_off);
     dst[0] = x[0];
     dst[1] = x[1];
   } else {
 #pragma unroll
     for (int w = 0; w < D / 32; w += 4) {
-      const u32x4 x = ld16(base, byte_off + 4 * w);
+      const u32x4 x = ld_kv16(base, byte_off + 4 * w);
       dst[w + 0] = x[0];
       dst[w + 1] = x[1];
       dst[w + 2] = x[2];
@@ -127,30 +159,16 @@ struct LaneOffsets {
   uint32_t token_bytes;   // bytes between consecutive tokens of a page
 };
 
+// Loads all 16 token rows of a chunk.  A chunk never crosses a page (page_size % 16 == 0),
+// so rows past the sequence end in the last chunk are unused slots of an allocated page;
+// they are discarded at process time by selects, never by arithmetic.
 template <int D>
 __device__ __forceinline__ void load_chunk(Chunk<D>& c, const uint16_t* kpage,
                                            const uint16_t* vpage, const LaneOffsets& lo) {
 #pragma unroll
-  for (int i = 0; i < D / 32; ++i) c.k[i] = ld16(kpage, lo.k + 64 * i);
+  for (int i = 0; i < D / 32; ++i) c.k[i] = ld_kv16(kpage, lo.k + 64 * i);
 #pragma unroll
   for (int r = 0; r < 4; ++r) load_v_row<D>(c.v[r], vpage, lo.v + r * lo.token_bytes);
-}
-
-// Tail chunk: V rows at or beyond `nvalid` are zero (never loaded), so garbage or NaN in the
-// unused slots of the last page cannot reach the PV product.  K is loaded whole (the chunk
-// lies inside an allocated page) and its scores are masked to -inf.
-template <int D>
-__device__ __forceinline__ void load_chunk_masked(Chunk<D>& c, const uint16_t* kpage,
-                                                  const uint16_t* vpage, const LaneOffsets& lo,
-                                                  int vrow0, int nvalid) {
-#pragma unroll
-  for (int i = 0; i < D / 32; ++i) c.k[i] = ld16(kpage, lo.k + 64 * i);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-#pragma unroll
-    for (int w = 0; w < D / 32; ++w) c.v[r][w] = 0u;
-    if (vrow0 + r < nvalid) load_v_row<D>(c.v[r], vpage, lo.v + r * lo.token_bytes);
-  }
 }
 
 template <int D>
@@ -160,6 +178,9 @@ struct SoftmaxState {
   float l;          // this lane's share of the running denominator
 };
 
+// One chunk of the online softmax.  kMasked: only the first `nvalid` tokens of the chunk are
+// real; the scores of the others become -inf and their V rows are replaced by zeros (so NaN or
+// Inf in unused page slots cannot reach the accumulators).
 template <int D, bool kMasked>
 __device__ __forceinline__ void process_chunk(SoftmaxState<D>& st, const Chunk<D>& c,
                                               const bf16x8 (&qop)[D / 32], float scale_log2,
@@ -195,13 +216,20 @@ __device__ __forceinline__ void process_chunk(SoftmaxState<D>& st, const Chunk<D
   const u32x2 pw = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
   const s16x4 pop = __builtin_bit_cast(s16x4, pw);
 
+  uint32_t v[4][D / 32];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const bool keep = !kMasked || (4 * g4 + r < nvalid);
+#pragma unroll
+    for (int w = 0; w < D / 32; ++w) v[r][w] = keep ? c.v[r][w] : 0u;
+  }
   // O^T[d][head] += V^T . P^T  (tile i covers dims (D/16)*m + i, m = 0..15)
 #pragma unroll
   for (int i = 0; i < D / 16; ++i) {
     const int w = i >> 1;
     const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
-    const u32x2 vw = {__builtin_amdgcn_perm(c.v[1][w], c.v[0][w], sel),
-                      __builtin_amdgcn_perm(c.v[3][w], c.v[2][w], sel)};
+    const u32x2 vw = {__builtin_amdgcn_perm(v[1][w], v[0][w], sel),
+                      __builtin_amdgcn_perm(v[3][w], v[2][w], sel)};
     st.o[i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, vw), pop,
                                                         st.o[i], 0, 0, 0);
   }
@@ -225,7 +253,12 @@ struct MainShape {
   float scale_log2;      // scale * log2(e)
 };
 
-template <int D>
+// Grid (Hkv, batch, splits): consecutive workgroup ids, which the dispatcher deals round-robin
+// to the 8 XCDs, walk the KV heads of one sequence first, then the sequences, then the splits.
+// Every XCD therefore gets an even share of the first split of every sequence (where ragged
+// batches keep most of their work), and the Hkv waves that read the same physical pages start
+// together.
+template <int D, int NBUF>
 __global__ __launch_bounds__(64) void mx_paged_decode_splitkv(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, uint16_t* __restrict__ out,
@@ -237,8 +270,8 @@ __global__ __launch_bounds__(64) void mx_paged_decode_splitkv(
   const int r16 = lane & 15;
   const int g4 = lane >> 4;
   const int kv = blockIdx.x;
-  const int split = blockIdx.y;
-  const int b = blockIdx.z;
+  const int b = blockIdx.y;
+  const int split = blockIdx.z;
   const int h = r16;  // head slot inside the group (valid when h < group)
   const bool hvalid = h < sh.group;
   const int qhead = kv * sh.group + h;
@@ -282,7 +315,8 @@ __global__ __launch_bounds__(64) void mx_paged_decode_splitkv(
   lo.v = 2u * (uint32_t)(4 * g4 * sh.token_stride + kv * D + VW * r16);
   bool bad_page = false;
 
-  // Element offset of chunk c (16 tokens) of this sequence inside the K/V pools.
+  // Element offset of chunk c (16 tokens) of this sequence inside the K/V pools.  Only table
+  // entries below ceil(seq / page_size) are ever read.
   auto chunk_base = [&](int c) -> int64_t {
     int pid = bt_row[c >> sh.chunk_shift];
     if (pid < 0 || (sh.num_pages > 0 && pid >= sh.num_pages)) {
@@ -299,52 +333,55 @@ __global__ __launch_bounds__(64) void mx_paged_decode_splitkv(
   st.l = 0.f;
 
   const int c0 = t0 / kChunk;
-  const int cf = t1 / kChunk;  // end of full chunks
-  const int tail = t1 - cf * kChunk;
+  const int c1 = (t1 + kChunk - 1) / kChunk;    // chunk range [c0, c1), last may be partial
+  const int last_valid = t1 - (c1 - 1) * kChunk; // tokens of chunk c1-1 (1..16)
   const float sl2 = sh.scale_log2;
+  auto nvalid_of = [&](int c) { return c == c1 - 1 ? last_valid : kChunk; };
 
-  Chunk<D> A, B;
-  auto load = [&](Chunk<D>& dst, int64_t base) {
-    load_chunk<D>(dst, kc + base, vc + base, lo);
-  };
+  Chunk<D> buf[NBUF];
+  auto load = [&](Chunk<D>& dst, int64_t base) { load_chunk<D>(dst, kc + base, vc + base, lo); };
 
-  // The page lookup of the chunk loaded next is issued before the current chunk's math so the
-  // scalar-load latency overlaps it.
-  int c = c0;
-  const int nfull = cf - c0;
-  if (nfull >= 2) {
-    load(A, chunk_base(c));
-    load(B, chunk_base(c + 1));
-    while (c + 3 < cf) {
-      const int64_t na = chunk_base(c + 2);
-      const int64_t nb = chunk_base(c + 3);
-      process_chunk<D, false>(st, A, qop, sl2, g4, kChunk);
-      load(A, na);
-      process_chunk<D, false>(st, B, qop, sl2, g4, kChunk);
-      load(B, nb);
-      c += 2;
+  // Register ring of NBUF chunks.  The steady-state loop processes NBUF full chunks and
+  // refills their buffers with the next NBUF, with no conditional loads (so the compiler's
+  // vmcnt waits stay partial); the page lookups of the refills are issued before the math.
+  const int n = c1 - c0;
+  if (n >= NBUF) {
+#pragma unroll
+    for (int i = 0; i < NBUF; ++i) load(buf[i], chunk_base(c0 + i));
+    int c = c0;
+    while (c + 2 * NBUF <= c1) {
+      int64_t nb[NBUF];
+#pragma unroll
+      for (int i = 0; i < NBUF; ++i) nb[i] = chunk_base(c + NBUF + i);
+#pragma unroll
+      for (int i = 0; i < NBUF; ++i) {
+        process_chunk<D, false>(st, buf[i], qop, sl2, g4, kChunk);
+        load(buf[i], nb[i]);
+      }
+      c += NBUF;
     }
-    if (c + 2 < cf) {
-      const int64_t na = chunk_base(c + 2);
-      process_chunk<D, false>(st, A, qop, sl2, g4, kChunk);
-      load(A, na);
-      process_chunk<D, false>(st, B, qop, sl2, g4, kChunk);
-      process_chunk<D, false>(st, A, qop, sl2, g4, kChunk);
-      c += 3;
-    } else {
-      process_chunk<D, false>(st, A, qop, sl2, g4, kChunk);
-      process_chunk<D, false>(st, B, qop, sl2, g4, kChunk);
-      c += 2;
+    // c + NBUF <= c1 < c + 2*NBUF: buffers hold chunks c .. c+NBUF-1, `extra` more remain.
+    const int extra = c1 - c - NBUF;
+#pragma unroll
+    for (int i = 0; i < NBUF; ++i) {
+      if (i < extra) {
+        const int64_t nbase = chunk_base(c + NBUF + i);
+        process_chunk<D, true>(st, buf[i], qop, sl2, g4, nvalid_of(c + i));
+        load(buf[i], nbase);
+      } else {
+        process_chunk<D, true>(st, buf[i], qop, sl2, g4, nvalid_of(c + i));
+      }
     }
-  } else if (nfull == 1) {
-    load(A, chunk_base(c));
-    process_chunk<D, false>(st, A, qop, sl2, g4, kChunk);
-    c += 1;
-  }
-  if (tail > 0) {
-    const int64_t base = chunk_base(c);
-    load_chunk_masked<D>(A, kc + base, vc + base, lo, 4 * g4, tail);
-    process_chunk<D, true>(st, A, qop, sl2, g4, tail);
+#pragma unroll
+    for (int i = 0; i < NBUF; ++i)
+      if (i < extra) process_chunk<D, true>(st, buf[i], qop, sl2, g4, nvalid_of(c + NBUF + i));
+  } else {
+#pragma unroll
+    for (int i = 0; i < NBUF; ++i)
+      if (i < n) load(buf[i], chunk_base(c0 + i));
+#pragma unroll
+    for (int i = 0; i < NBUF; ++i)
+      if (i < n) process_chunk<D, true>(st, buf[i], qop, sl2, g4, nvalid_of(c0 + i));
   }
 
   if (bad_page && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
@@ -470,10 +507,17 @@ int ok() {
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int64_t align_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 
-// Split policy constants (replace the 104-SM regime table of submission_clean.cu:375-430).
-constexpr int64_t kWavesPerCU = 16;           // single-wave workgroups requested per CU
-constexpr int64_t kMinTokensPerSplit = 256;   // amortises Q load, pipeline fill and partials
+// Split policy (replaces the 104-SM regime table of submission_clean.cu:375-430).  Measured
+// on MI355X: the split-KV kernel reaches the device's streaming-read ceiling once about
+// 8 MB of K/V loads are in flight, i.e. 2 single-wave workgroups per CU for D=128 (8 KB per
+// 16-token chunk, 2 chunks in flight per wave) and 4 per CU for D=64 (4 KB chunks) and
+// D=256 (one wave per SIMD, issue-bound).  Every extra split costs a wave prologue and a
+// partial write, so the policy asks for just enough splits to reach that wave count.
+constexpr int64_t kMinTokensPerSplit = 128;   // amortises Q load, pipeline fill and partials
+constexpr int64_t kMaxTokensPerSplit = 4096;  // bounds one wave's share of a long sequence
 constexpr int64_t kMaxGridDim = 65535;
+
+int64_t target_waves_per_cu(int64_t head_dim) { return head_dim == 128 ? 2 : 4; }
 
 struct Plan {
   int64_t splits = 1;
@@ -546,9 +590,11 @@ int make_plan(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t he
       if (st != MX_STATUS_OK) return st;
     }
     const int64_t units = batch * num_kv_heads;
-    ns = ceil_div(num_cus * kWavesPerCU, units);
+    ns = ceil_div(num_cus * target_waves_per_cu(head_dim), units);
     const int64_t max_by_len = ceil_div(cap, kMinTokensPerSplit);
     if (ns > max_by_len) ns = max_by_len;
+    const int64_t min_by_len = ceil_div(cap, kMaxTokensPerSplit);
+    if (ns < min_by_len) ns = min_by_len;
   }
   if (ns > cap_pages) ns = cap_pages;
   if (ns < 1) ns = 1;
@@ -636,8 +682,8 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
     sh.tokens_per_split = (int)plan.tokens_per_split;
     sh.cap_tokens = (int)plan.cap_tokens;
     sh.scale_log2 = scale * 1.4426950408889634f;
-    const dim3 grid((unsigned)num_kv_heads, (unsigned)plan.splits, (unsigned)batch);
-    hipLaunchKernelGGL(mx_paged_decode_splitkv<D>, grid, dim3(64), 0, stream,
+    const dim3 grid((unsigned)num_kv_heads, (unsigned)batch, (unsigned)plan.splits);
+    hipLaunchKernelGGL((mx_paged_decode_splitkv<D, ring_depth<D>()>), grid, dim3(64), 0, stream,
                        static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                        static_cast<const uint16_t*>(v), static_cast<uint16_t*>(out), seq_lens,
                        block_table, part_o, part_lse, reinterpret_cast<uint32_t*>(ws), sh);

@@ -123,6 +123,44 @@ def paged_gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     return out
 
 
+class BoundDecode:
+    """A decode call with its C arguments prepared once (tight loops, benchmarks, graphs).
+
+    ``__call__(phase=0)`` issues the launch(es) on the bound stream and raises on a bad
+    status.  The bound tensors must stay alive and keep their storage.
+    """
+
+    def __init__(self, q, k_cache, v_cache, block_table, seq_lens, scale=None, *, out=None,
+                 num_splits: int = 0, max_seq_len: int = 0, workspace=None, stream=None):
+        # validate once through the tensor-level entry (phase 0 runs a real call)
+        self.out = paged_gqa_decode(q, k_cache, v_cache, block_table, seq_lens, scale, out=out,
+                                    num_splits=num_splits, max_seq_len=max_seq_len,
+                                    workspace=workspace, stream=stream)
+        q3 = q.view(q.shape[0], q.shape[2], q.shape[3]) if q.dim() == 4 else q
+        B, Hq, D = q3.shape
+        num_pages, P, Hkv, _ = k_cache.shape
+        if scale is None:
+            scale = 1.0 / math.sqrt(D)
+        self.plan = plan(B, Hq, Hkv, D, P, block_table.shape[1], max_seq_len, num_splits)
+        self._keep = (q3, k_cache, v_cache, block_table, seq_lens, workspace)
+        ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        self._fn = _lib.load().mx_paged_gqa_decode
+        self._args = [_ptr(q3), _ptr(k_cache), _ptr(v_cache), _ptr(self.out), _ptr(seq_lens),
+                      _ptr(block_table), B, Hq, Hkv, D, P, num_pages, block_table.shape[1],
+                      max_seq_len, float(scale), num_splits, _ptr(workspace), ws_bytes]
+        self._stream = _stream_handle(stream, q.device)
+
+    @property
+    def splits(self) -> int:
+        return self.plan["splits"]
+
+    def __call__(self, phase: int = 0) -> torch.Tensor:
+        st = self._fn(*self._args, phase, self._stream)
+        if st != _lib.MX_STATUS_OK:
+            _lib.check(st)
+        return self.out
+
+
 def run_kernel(q, k_cache_paged, v_cache_paged, output, cache_seqlens, block_table,
                batch_size, seqlen_k, seqlen_q, num_heads, num_heads_k, headdim,
                page_block_size, num_blocks, causal) -> None:

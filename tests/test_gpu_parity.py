@@ -231,3 +231,32 @@ def test_c500_case_via_run_kernel(case, table):
     matched = (diff <= tol).float().mean().item()
     assert not bool((diff > 8 * tol).any())
     assert matched >= (1.0 if case <= 3 else 0.99)
+
+
+# ------------------------------------------------------------------------------------------
+# Golden fixtures (expected outputs from the fp64 brute force, tests/golden/make_golden.py)
+# ------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["task_example", "ragged_g7_p64_d64"])
+@pytest.mark.parametrize("ns", [0, 1, 4])
+def test_golden_fixtures(name, ns):
+    from test_oracle import load_golden
+
+    inp, expected = load_golden(name)
+    inp = inp.to(DEV)
+    out = _decode(inp, num_splits=ns)
+    assert_close_to_oracle(out, expected, f"{name} ns={ns}")
+
+
+def test_golden_task_example_through_run_kernel():
+    """task.md's example through the 15-argument entry (num_blocks = B * row width)."""
+    from test_oracle import load_golden
+
+    inp, expected = load_golden("task_example")
+    inp = inp.to(DEV)
+    out = torch.zeros_like(inp.q)
+    B, W_ = inp.block_table.shape
+    run_kernel(inp.q, inp.k_cache, inp.v_cache, out, inp.seq_lens, inp.block_table,
+               B, 512, 1, 32, 4, 128, 16, B * W_, 0)
+    torch.cuda.synchronize()
+    assert_close_to_oracle(out, expected, "task_example run_kernel")

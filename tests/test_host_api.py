@@ -1,0 +1,188 @@
+"""Host-side checks of libmxattn.so that need no GPU.
+
+* the library loads and exports every function include/mx_paged_decode.h declares;
+* argument validation returns the documented status before any HIP call (reference
+  run_kernel validates nothing, submission_clean.cu:432-504; the original LSE kernel silently
+  returns on unsupported shapes, optimized_c500_flash_attn.cu:890-900);
+* the split planner (replacing submission_clean.cu:375-430, 456-461) keeps its invariants.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import re
+import subprocess
+
+import pytest
+
+from conftest import gpu_available
+from mx_flash_attn_kernel_opt__amd import MXAttnError, _lib, plan
+from mx_flash_attn_kernel_opt__amd import workloads as W
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "mx_paged_decode.h")
+
+
+def header_functions() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*(?:const\s+)?(?:void|int|int64_t|char)\s*\*?\s*(\w+)\s*\(",
+                      text, flags=re.M)
+
+
+def test_header_declares_the_drop_in_and_extended_entry_points():
+    fns = header_functions()
+    for name in ("run_kernel", "mx_paged_gqa_decode", "mx_paged_gqa_decode_plan",
+                 "mx_paged_gqa_decode_workspace_size", "mx_read_device_status",
+                 "mx_last_status", "mx_last_error", "mx_version"):
+        assert name in fns
+    assert set(fns) == set(_lib.SIGNATURES), "ctypes binding and header disagree"
+
+
+def test_library_exports_every_header_symbol():
+    lib = _lib.load()
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.library_path()],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if ln.strip()}
+    for name in header_functions():
+        assert name in exported, f"{name} not exported"
+        assert getattr(lib, name) is not None
+    assert b"gfx950" in lib.mx_version()
+
+
+def test_run_kernel_abi_matches_the_reference_binding():
+    # verify_real.py:12-14: argtypes [c_void_p]*6 + [c_int64]*9, restype None
+    restype, argtypes = _lib.SIGNATURES["run_kernel"]
+    assert restype is None
+    assert argtypes == [ctypes.c_void_p] * 6 + [ctypes.c_int64] * 9
+
+
+# ------------------------------------------------------------------------------------------
+# Validation (no HIP call is reached on these paths)
+# ------------------------------------------------------------------------------------------
+
+FAKE = ctypes.c_void_p(0x1000)   # never dereferenced: validation fails first
+
+
+def _decode(**over):
+    args = dict(q=FAKE, k=FAKE, v=FAKE, out=FAKE, lens=FAKE, table=FAKE, B=2, Hq=32, Hkv=8,
+                D=128, P=16, pages=64, max_pages=32, max_seq=0, scale=0.088, ns=2,
+                ws=FAKE, ws_bytes=1 << 30, phase=0, stream=None)
+    args.update(over)
+    lib = _lib.load()
+    return lib.mx_paged_gqa_decode(args["q"], args["k"], args["v"], args["out"], args["lens"],
+                                   args["table"], args["B"], args["Hq"], args["Hkv"], args["D"],
+                                   args["P"], args["pages"], args["max_pages"], args["max_seq"],
+                                   args["scale"], args["ns"], args["ws"], args["ws_bytes"],
+                                   args["phase"], args["stream"])
+
+
+@pytest.mark.parametrize("field", ["q", "k", "v", "out", "lens", "table"])
+def test_null_pointers_are_rejected(field):
+    assert _decode(**{field: None}) == _lib.MX_STATUS_NULL_POINTER
+    assert "non-NULL" in _lib.load().mx_last_error().decode()
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(Hq=30, Hkv=8), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(B=0), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(Hkv=0), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(max_pages=0), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(pages=-1), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(ns=-3), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(D=96), _lib.MX_STATUS_UNSUPPORTED),
+    (dict(D=512), _lib.MX_STATUS_UNSUPPORTED),
+    (dict(P=8), _lib.MX_STATUS_UNSUPPORTED),
+    (dict(P=48), _lib.MX_STATUS_UNSUPPORTED),
+    (dict(Hq=64, Hkv=2), _lib.MX_STATUS_UNSUPPORTED),     # group 32 > 16
+    (dict(B=70000), _lib.MX_STATUS_UNSUPPORTED),
+    (dict(phase=3), _lib.MX_STATUS_INVALID_ARGUMENT),
+    (dict(scale=float("nan")), _lib.MX_STATUS_INVALID_ARGUMENT),
+    (dict(scale=float("inf")), _lib.MX_STATUS_INVALID_ARGUMENT),
+    (dict(ws_bytes=100), _lib.MX_STATUS_WORKSPACE_TOO_SMALL),
+])
+def test_invalid_arguments_return_status(over, status):
+    assert _decode(**over) == status
+    assert _lib.load().mx_last_status() == status
+    assert _lib.load().mx_last_error()
+
+
+def _run_kernel(**over):
+    a = dict(B=4, seqlen_k=512, seqlen_q=1, Hq=32, Hkv=8, D=128, P=16, nb=128, causal=0)
+    a.update(over)
+    lib = _lib.load()
+    lib.run_kernel(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, a["B"], a["seqlen_k"], a["seqlen_q"],
+                   a["Hq"], a["Hkv"], a["D"], a["P"], a["nb"], a["causal"])
+    return lib.mx_last_status()
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(seqlen_q=2), _lib.MX_STATUS_UNSUPPORTED),
+    (dict(causal=1), _lib.MX_STATUS_UNSUPPORTED),
+    (dict(nb=130), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(nb=2), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(seqlen_k=0), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(Hq=32, Hkv=5), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(D=100), _lib.MX_STATUS_UNSUPPORTED),
+])
+def test_run_kernel_rejects_what_the_reference_ignores(over, status, capfd):
+    assert _run_kernel(**over) == status
+    assert "run_kernel" in capfd.readouterr().err
+
+
+@pytest.mark.skipif(gpu_available(), reason="checks the no-device path")
+def test_automatic_plan_without_a_device_reports_hip_error():
+    assert _decode(ns=0) == _lib.MX_STATUS_HIP_ERROR
+
+
+def test_python_wrapper_raises_with_status():
+    with pytest.raises(MXAttnError) as e:
+        plan(2, 30, 8, 128, 16, 32, num_cus=256)
+    assert e.value.status == _lib.MX_STATUS_INVALID_SHAPE
+
+
+# ------------------------------------------------------------------------------------------
+# Planner invariants
+# ------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,P,max_pages,cap,ns_req", [
+    (64, 32, 8, 128, 16, 256, 0, 0),
+    (1, 64, 8, 128, 16, 8192, 0, 0),
+    (256, 28, 4, 128, 64, 128, 0, 0),
+    (4, 32, 8, 128, 16, 32, 512, 0),
+    (3, 32, 8, 128, 16, 40, 300, 0),
+    (8, 32, 8, 64, 32, 100, 0, 7),
+    (2, 16, 2, 256, 16, 10, 0, 1000),
+    (1, 32, 4, 128, 16, 1, 1, 0),
+])
+def test_plan_invariants(B, Hq, Hkv, D, P, max_pages, cap, ns_req):
+    p = plan(B, Hq, Hkv, D, P, max_pages, cap, ns_req, num_cus=256)
+    ns, tps, ws = p["splits"], p["tokens_per_split"], p["workspace_bytes"]
+    table_tokens = max_pages * P
+    eff_cap = cap if 0 < cap < table_tokens else table_tokens
+    cap_pages = math.ceil(eff_cap / P)
+    assert 1 <= ns <= cap_pages
+    assert tps % P == 0 and tps >= P
+    assert ns * tps >= eff_cap                      # every capacity token is covered
+    assert (ns - 1) * tps < eff_cap                 # and no split is empty at capacity
+    if ns_req > 0:
+        assert ns <= ns_req
+    if ns == 1:
+        assert ws == 256
+    else:
+        rows = B * Hq * ns
+        assert ws == 256 + math.ceil(rows * 4 / 256) * 256 + rows * D * 4
+
+
+def test_policy_on_the_north_star_configs():
+    """Split counts the automatic policy picks for a 256-CU MI355X (measured optima: see the
+    split sweep in the design notes)."""
+    expect = {"llama3_8b": 1, "long_b1_128k": 64, "long_b4_32k": 16, "sweep_d64": 2,
+              "sweep_d256": 8}
+    for name, ns in expect.items():
+        s = W.NORTH_STAR[name]
+        got = plan(s.batch, s.num_heads, s.num_kv_heads, s.head_dim, s.page_size, s.max_pages,
+                   num_cus=256)["splits"]
+        assert got == ns, f"{name}: {got} != {ns}"
