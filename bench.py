@@ -6,10 +6,11 @@
 One step = one decode-attention call over the whole batch of the workload (default: the
 Llama-3-8B decode shape the metric is quoted on, B=64 Hq=32 Hkv=8 D=128 P=16 L=4096), inputs
 resident in HBM.  The timed region is K back-to-back steps on one stream, bracketed by
-torch.cuda.synchronize(); inside it HIP events bracket the split-KV kernel of every step (the
-combine kernel, when the plan has one, runs after the second event).  Prints ONE JSON line:
+torch.cuda.synchronize(); inside it HIP events bracket the main kernel of every step (the
+balanced single launch, or the split-KV kernel of the split grid, whose combine kernel runs
+after the second event).  Prints ONE JSON line:
   value      effective KV GB/s of whole steps = algorithmic K+V bytes / (ms_per_step)
-  roofline   achieved GB/s of the split-KV kernel alone (events around it) against 8 TB/s
+  roofline   achieved GB/s of the main kernel alone (events around it) against 8 TB/s
   cpu_baseline  the fp32 oracle (oracle/paged_attention.py) timed on this host on a bounded
              sample of the same workload.
 ``--all`` prints one extra JSON line per north-star configuration (no CPU baseline).
@@ -52,10 +53,10 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def _traffic_from_profile(workload: str):
-    """HBM bytes per launch of the split-KV kernel, from the committed rocprofv3 --pmc summary
-    (profiles/splitkv_<workload>_traffic.md, line 'traffic_bytes_per_launch: N'), or None."""
-    path = os.path.join(PROFILE_DIR, f"splitkv_{workload}_traffic.md")
+def _traffic_from_profile(kernel: str, workload: str):
+    """HBM bytes per launch of the main kernel, from the committed rocprofv3 --pmc summary
+    (profiles/<kernel>_<workload>_traffic.md, line 'traffic_bytes_per_launch: N'), or None."""
+    path = os.path.join(PROFILE_DIR, f"{kernel}_{workload}_traffic.md")
     try:
         with open(path) as f:
             m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read())
@@ -186,17 +187,20 @@ def result_line(args, spec, r, cpu=None) -> dict:
             "num_kv_heads": spec.num_kv_heads, "head_dim": spec.head_dim,
             "page_size": spec.page_size, "max_pages": spec.max_pages,
             "seq_lens": spec.seq_lens, "seq_args": list(spec.seq_args),
-            "kv_bytes": r["nbytes"], "splits": r["plan"]["splits"],
+            "kv_bytes": r["nbytes"], "schedule": r["plan"]["schedule"],
+            "workgroups": r["plan"]["workgroups"], "splits": r["plan"]["splits"],
             "tokens_per_split": r["plan"]["tokens_per_split"], "kv_pools": r["pools"],
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "mx_paged_decode_splitkv",
+            "kernel": ("mx_paged_decode_balanced" if r["plan"]["schedule"] == "balanced"
+                       else "mx_paged_decode_splitkv"),
             "achieved": round(r["kernel_gbps"], 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(frac, 4),
-            "traffic": _traffic_from_profile(spec.name),
+            "traffic": _traffic_from_profile(
+                "balanced" if r["plan"]["schedule"] == "balanced" else "splitkv", spec.name),
             "kernel_us_mean": round(r["kernel_us_mean"], 2),
             "kernel_us_median": round(r["kernel_us_median"], 2),
         },

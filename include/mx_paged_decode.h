@@ -46,9 +46,17 @@ extern "C" {
 #define MX_DEVICE_BAD_PAGE_ID 1u    /* a valid block_table slot held an id outside [0, num_pages) */
 #define MX_DEVICE_SEQ_TOO_LONG 2u   /* seq_lens[b] exceeded the capacity the call was planned for */
 
+/* Schedules reported by mx_paged_gqa_decode_plan. */
+#define MX_SCHEDULE_SPLIT_GRID 0   /* grid (Hkv, batch, splits) + combine kernel when splits > 1  */
+#define MX_SCHEDULE_BALANCED 1     /* one launch of a fixed number of workgroups that divide the
+                                      batch's K/V chunks evenly from seq_lens on the device and
+                                      merge split sequences themselves                            */
+
 /* Phase flags for mx_paged_gqa_decode (0 = run everything). */
-#define MX_PHASE_MAIN_ONLY 1        /* run only the split-KV kernel; partials stay in workspace */
-#define MX_PHASE_COMBINE_ONLY 2     /* run only the combine over partials of an identical call  */
+#define MX_PHASE_MAIN_ONLY 1        /* split grid: run only the split-KV kernel, partials stay in
+                                       the workspace (balanced schedule: the whole call)          */
+#define MX_PHASE_COMBINE_ONLY 2     /* split grid: run only the combine over the partials of an
+                                       identical MAIN_ONLY call (balanced schedule: nothing)      */
 
 /*
  * Drop-in replacement for the reference's C500 kernel entry point, same name, argument order
@@ -78,10 +86,16 @@ void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_pa
  *                      seq_lens[b] beyond the planned capacity (max_seq_len rounded up to whole
  *                      splits, at most max_pages_per_seq*page_size) are clamped and flagged
  *                      (MX_DEVICE_SEQ_TOO_LONG).
- *   num_splits         0 = automatic policy, otherwise the requested split count (clamped to
- *                      the number of pages of max_seq_len).
+ *   num_splits         0 = automatic: the balanced schedule when batch <= 512 and
+ *                      64 <= batch * num_kv_heads <= 8192, else the split grid with a
+ *                      CU-count-driven split count;
+ *                      > 0 = split grid with that many splits per sequence (clamped to the
+ *                      number of pages of max_seq_len);
+ *                      < 0 = balanced schedule with exactly -num_splits workgroups.
  *   workspace          device memory of >= mx_paged_gqa_decode_workspace_size() bytes,
- *                      zero-filled once by the caller before first use; NULL = library-owned.
+ *                      zero-filled once by the caller before first use (its first 196 864
+ *                      bytes hold a status word and merge counters that every call leaves at
+ *                      zero); NULL = library-owned.
  *   phase              0, MX_PHASE_MAIN_ONLY or MX_PHASE_COMBINE_ONLY.
  *   stream             hipStream_t (NULL = legacy default stream).
  * Returns MX_STATUS_OK or a negative MX_STATUS_* code; nothing is launched on error.
@@ -94,16 +108,18 @@ int mx_paged_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
                         int64_t workspace_bytes, int32_t phase, void* stream);
 
 /*
- * Host-only planning (no HIP call when num_cus > 0): validates the shape and reports the split
- * count, tokens per split and workspace bytes a call with these arguments would use.  Replaces
- * the reference's split policy choose_num_splits (submission_clean.cu:375-430) and its
- * page-rounding of splits (submission_clean.cu:456-461).  num_cus <= 0 queries the current
- * device.  Any of the out pointers may be NULL.
+ * Host-only planning (no HIP call when num_cus > 0): validates the shape and reports the
+ * schedule (MX_SCHEDULE_*), the splits per sequence and tokens per split (split grid; 0 for the
+ * balanced schedule), the workgroups launched and the workspace bytes a call with these
+ * arguments would use.  Replaces the reference's split policy choose_num_splits
+ * (submission_clean.cu:375-430) and its page-rounding of splits (submission_clean.cu:456-461).
+ * num_cus <= 0 queries the current device.  Any of the out pointers may be NULL.
  */
 int mx_paged_gqa_decode_plan(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
                              int64_t head_dim, int64_t page_size, int64_t max_pages_per_seq,
                              int64_t max_seq_len, int64_t num_splits, int64_t num_cus,
-                             int64_t* splits_out, int64_t* tokens_per_split_out,
+                             int64_t* schedule_out, int64_t* splits_out,
+                             int64_t* tokens_per_split_out, int64_t* workgroups_out,
                              int64_t* workspace_bytes_out);
 
 /* Workspace bytes a call needs (replaces the grow-only sizing of submission_clean.cu:463,

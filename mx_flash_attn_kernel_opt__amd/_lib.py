@@ -27,6 +27,9 @@ MX_STATUS_INVALID_ARGUMENT = -7
 MX_DEVICE_BAD_PAGE_ID = 1
 MX_DEVICE_SEQ_TOO_LONG = 2
 
+MX_SCHEDULE_SPLIT_GRID = 0
+MX_SCHEDULE_BALANCED = 1
+
 MX_PHASE_ALL = 0
 MX_PHASE_MAIN_ONLY = 1
 MX_PHASE_COMBINE_ONLY = 2
@@ -52,7 +55,7 @@ SIGNATURES = {
         ctypes.c_int,
         [_VP] * 6 + [_I64] * 8 + [_F32, _I64, _VP, _I64, _I32, _VP],
     ),
-    "mx_paged_gqa_decode_plan": (ctypes.c_int, [_I64] * 9 + [_P64, _P64, _P64]),
+    "mx_paged_gqa_decode_plan": (ctypes.c_int, [_I64] * 9 + [_P64] * 5),
     "mx_paged_gqa_decode_workspace_size": (ctypes.c_int64, [_I64] * 8),
     "mx_read_device_status": (ctypes.c_int, [_VP, _I32, _VP, _P32]),
     "mx_last_status": (ctypes.c_int, []),

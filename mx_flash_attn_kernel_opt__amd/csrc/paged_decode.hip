@@ -51,7 +51,15 @@ typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
 
 constexpr int kChunk = 16;             // tokens per PV k-step (one 16x16x16 MFMA)
 constexpr float kRescaleSlack = 8.0f;  // log2 units the stale running max may lag behind
-constexpr int kStatusBytes = 256;      // device status word region at the start of a workspace
+// Workspace layout: [status word region][merge counters][partials].  The counter region has
+// a fixed size and offset and only the balanced kernel touches it (it resets every counter it
+// uses), so a zero-filled workspace keeps valid counters across calls of any shape, whatever
+// the partials of earlier calls left behind.
+constexpr int kStatusBytes = 256;
+constexpr int kMaxSlots = 4096 + 8192;          // balanced: workgroups + batch * Hkv
+constexpr int kCounterLevels = 4;               // fan-in-8 merge tree levels
+constexpr int64_t kCounterBytes = (int64_t)kCounterLevels * kMaxSlots * 4;
+constexpr int64_t kPartialBase = kStatusBytes + kCounterBytes;
 
 // ------------------------------------------------------------------------------------------
 // Device helpers
@@ -95,10 +103,41 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 #define MX_NBUF_D128 2
 #endif
 #ifndef MX_NBUF_D256
-#define MX_NBUF_D256 2
+#define MX_NBUF_D256 1
 #endif
-#ifndef MX_KV_NONTEMPORAL
-#define MX_KV_NONTEMPORAL 0
+#ifndef MX_K_NONTEMPORAL
+#define MX_K_NONTEMPORAL 1
+#endif
+#ifndef MX_V_NONTEMPORAL
+#define MX_V_NONTEMPORAL 1
+#endif
+#ifndef MX_K_VIA_LDS_D64
+#define MX_K_VIA_LDS_D64 1
+#endif
+#ifndef MX_K_VIA_LDS_D128
+#define MX_K_VIA_LDS_D128 1
+#endif
+#ifndef MX_K_VIA_LDS_D256
+#define MX_K_VIA_LDS_D256 1
+#endif
+#ifndef MX_NW_D64
+#define MX_NW_D64 2
+#endif
+#ifndef MX_NW_D128
+#define MX_NW_D128 4
+#endif
+#ifndef MX_NW_D256
+#define MX_NW_D256 4
+#endif
+// Minimum waves per SIMD the register allocator must allow (1 = no cap).
+#ifndef MX_WAVES_PER_EU_D64
+#define MX_WAVES_PER_EU_D64 2
+#endif
+#ifndef MX_WAVES_PER_EU_D128
+#define MX_WAVES_PER_EU_D128 2
+#endif
+#ifndef MX_WAVES_PER_EU_D256
+#define MX_WAVES_PER_EU_D256 1
 #endif
 
 template <int D>
@@ -106,22 +145,31 @@ constexpr int ring_depth() {
   return D == 64 ? MX_NBUF_D64 : (D == 128 ? MX_NBUF_D128 : MX_NBUF_D256);
 }
 
-// K/V stream loads: wave-uniform base plus per-lane byte offset.
+// Whether K chunks are staged through LDS (see k_lane_offsets).
+template <int D>
+constexpr bool k_via_lds() {
+  return (D == 64 ? MX_K_VIA_LDS_D64 : (D == 128 ? MX_K_VIA_LDS_D128 : MX_K_VIA_LDS_D256)) != 0;
+}
+
+// Waves per workgroup of the split-KV kernel.
+template <int D>
+constexpr int waves_per_group() {
+  return D == 64 ? MX_NW_D64 : (D == 128 ? MX_NW_D128 : MX_NW_D256);
+}
+
+// K/V stream loads: wave-uniform base plus per-lane byte offset.  NT selects the
+// nontemporal (streaming) cache policy.
+template <bool NT>
 __device__ __forceinline__ u32x4 ld_kv16(const uint16_t* base, uint32_t byte_off) {
   const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + byte_off);
-#if MX_KV_NONTEMPORAL
-  return __builtin_nontemporal_load(p);
-#else
+  if constexpr (NT) return __builtin_nontemporal_load(p);
   return *p;
-#endif
 }
+template <bool NT>
 __device__ __forceinline__ u32x2 ld_kv8(const uint16_t* base, uint32_t byte_off) {
   const u32x2* p = reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(base) + byte_off);
-#if MX_KV_NONTEMPORAL
-  return __builtin_nontemporal_load(p);
-#else
+  if constexpr (NT) return __builtin_nontemporal_load(p);
   return *p;
-#endif
 }
 
 // Register image of one 16-token chunk of one KV head.
@@ -137,13 +185,13 @@ template <int D>
 __device__ __forceinline__ void load_v_row(uint32_t (&dst)[D / 32], const uint16_t* base,
                                            uint32_t byte_off) {
   if constexpr (D == 64) {
-    const u32x2 x = ld_kv8(base, byte_off);
+    const u32x2 x = ld_kv8<MX_V_NONTEMPORAL != 0>(base, byte_off);
     dst[0] = x[0];
     dst[1] = x[1];
   } else {
 #pragma unroll
     for (int w = 0; w < D / 32; w += 4) {
-      const u32x4 x = ld_kv16(base, byte_off + 4 * w);
+      const u32x4 x = ld_kv16<MX_V_NONTEMPORAL != 0>(base, byte_off + 4 * w);
       dst[w + 0] = x[0];
       dst[w + 1] = x[1];
       dst[w + 2] = x[2];
@@ -154,10 +202,36 @@ __device__ __forceinline__ void load_v_row(uint32_t (&dst)[D / 32], const uint16
 
 // Per-lane byte offsets of a chunk inside its page (constant for the whole wave).
 struct LaneOffsets {
-  uint32_t k;             // K[token r16][8*g4]
+  uint32_t k;             // first K load of this lane
+  uint32_t k_step;        // byte step between the lane's successive K loads
   uint32_t v;             // V[token 4*g4][(D/16)*r16]
   uint32_t token_bytes;   // bytes between consecutive tokens of a page
 };
+
+// K chunk staging.  Direct (k_via_lds<D>() false): lane (r16, g4) loads K[r16][32i + 8g4 .. +7]
+// straight into the MFMA A operand: each load instruction touches 16 rows x 64 B.
+// Through LDS (k_via_lds<D>() true): lane j loads row i*RPI + j/SPR, 16-byte segment j%SPR of
+// the chunk (RPI = 512/D whole 2D-byte rows per instruction, the V access pattern), writes it
+// to a wave-private 16 x 2D-byte LDS tile at an XOR-swizzled segment, and reads the A operand
+// back with ds_read_b128; the swizzle keeps both the writes and the 16 rows of one read
+// conflict-free.
+template <int D>
+__device__ __forceinline__ int k_swizzle(int row) {
+  return D == 64 ? ((row >> 1) & 7) : (row & 15);
+}
+
+template <int D>
+__device__ __forceinline__ void k_lane_offsets(LaneOffsets& lo, int lane, int kv) {
+  if constexpr (k_via_lds<D>()) {
+    constexpr int SPR = D / 8;     // 16-byte segments per K row
+    constexpr int RPI = 64 / SPR;  // rows per load instruction
+    lo.k = (uint32_t)(lane / SPR) * lo.token_bytes + 2u * (uint32_t)(kv * D) + 16u * (lane % SPR);
+    lo.k_step = RPI * lo.token_bytes;
+  } else {
+    lo.k = (uint32_t)(lane & 15) * lo.token_bytes + 2u * (uint32_t)(kv * D) + 16u * (lane >> 4);
+    lo.k_step = 64u;
+  }
+}
 
 // Loads all 16 token rows of a chunk.  A chunk never crosses a page (page_size % 16 == 0),
 // so rows past the sequence end in the last chunk are unused slots of an allocated page;
@@ -166,9 +240,39 @@ template <int D>
 __device__ __forceinline__ void load_chunk(Chunk<D>& c, const uint16_t* kpage,
                                            const uint16_t* vpage, const LaneOffsets& lo) {
 #pragma unroll
-  for (int i = 0; i < D / 32; ++i) c.k[i] = ld_kv16(kpage, lo.k + 64 * i);
+  for (int i = 0; i < D / 32; ++i)
+    c.k[i] = ld_kv16<MX_K_NONTEMPORAL != 0>(kpage, lo.k + (uint32_t)i * lo.k_step);
 #pragma unroll
   for (int r = 0; r < 4; ++r) load_v_row<D>(c.v[r], vpage, lo.v + r * lo.token_bytes);
+}
+
+// A operands of the QK MFMAs for one chunk (see k_lane_offsets for the two stagings).
+template <int D>
+__device__ __forceinline__ void k_operands(bf16x8 (&kop)[D / 32], const Chunk<D>& c,
+                                           char* klds, int lane) {
+  if constexpr (k_via_lds<D>()) {
+    constexpr int SPR = D / 8;
+    constexpr int RPI = 64 / SPR;
+    const int wr = lane / SPR;
+    const int ws = lane % SPR;
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) {
+      const int row = i * RPI + wr;
+      *reinterpret_cast<u32x4*>(klds + row * 2 * D + 16 * (ws ^ k_swizzle<D>(row))) = c.k[i];
+    }
+    const int t = lane & 15;
+    const int g4 = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i)
+      kop[i] = __builtin_bit_cast(
+          bf16x8, *reinterpret_cast<const u32x4*>(klds + t * 2 * D +
+                                                  16 * ((4 * i + g4) ^ k_swizzle<D>(t))));
+  } else {
+    (void)klds;
+    (void)lane;
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) kop[i] = __builtin_bit_cast(bf16x8, c.k[i]);
+  }
 }
 
 template <int D>
@@ -184,13 +288,14 @@ struct SoftmaxState {
 template <int D, bool kMasked>
 __device__ __forceinline__ void process_chunk(SoftmaxState<D>& st, const Chunk<D>& c,
                                               const bf16x8 (&qop)[D / 32], float scale_log2,
-                                              int g4, int nvalid) {
+                                              int g4, int nvalid, char* klds, int lane) {
   // S^T[token][head] = K . Q^T  (16 tokens x 16 head slots, contraction over D)
+  bf16x8 kop[D / 32];
+  k_operands<D>(kop, c, klds, lane);
   f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < D / 32; ++i)
-    s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, c.k[i]), qop[i], s, 0,
-                                                 0, 0);
+    s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[i], qop[i], s, 0, 0, 0);
   float x[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -236,87 +341,80 @@ __device__ __forceinline__ void process_chunk(SoftmaxState<D>& st, const Chunk<D
 }
 
 // ------------------------------------------------------------------------------------------
-// Main split-KV kernel
+// Shared pieces of the main kernels
 // ------------------------------------------------------------------------------------------
 
 struct MainShape {
   int64_t page_stride;   // elements between physical pages: page_size * Hkv * D
   int token_stride;      // elements between tokens of a page: Hkv * D
   int num_heads;
+  int num_kv_heads;
   int group;
+  int batch;
   int max_pages;         // block_table row width
   int num_pages;         // pool size, 0 = unknown
   int chunk_shift;       // log2(page_size / 16)
-  int num_splits;
-  int tokens_per_split;  // multiple of page_size
   int cap_tokens;        // seq_lens above this are clamped and flagged
   float scale_log2;      // scale * log2(e)
+  // split grid
+  int num_splits;
+  int tokens_per_split;  // multiple of page_size
+  // balanced schedule
+  int num_groups;        // workgroups of the launch
+  int unit_overhead;     // positions charged per (sequence, KV head) on top of its chunks
+  int num_slots;         // partial slots: num_groups + batch * Hkv
 };
 
-// Grid (Hkv, batch, splits): consecutive workgroup ids, which the dispatcher deals round-robin
-// to the 8 XCDs, walk the KV heads of one sequence first, then the sequences, then the splits.
-// Every XCD therefore gets an even share of the first split of every sequence (where ragged
-// batches keep most of their work), and the Hkv waves that read the same physical pages start
-// together.
-template <int D, int NBUF>
-__global__ __launch_bounds__(64) void mx_paged_decode_splitkv(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
-    const uint16_t* __restrict__ vc, uint16_t* __restrict__ out,
-    const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ block_table,
-    float* __restrict__ part_o, float* __restrict__ part_lse, uint32_t* __restrict__ status,
-    const MainShape sh) {
-  constexpr int VW = D / 16;  // dims per lane per V row == number of PV tiles
-  const int lane = threadIdx.x;
-  const int r16 = lane & 15;
-  const int g4 = lane >> 4;
-  const int kv = blockIdx.x;
-  const int b = blockIdx.y;
-  const int split = blockIdx.z;
-  const int h = r16;  // head slot inside the group (valid when h < group)
-  const bool hvalid = h < sh.group;
-  const int qhead = kv * sh.group + h;
-
+// Sequence length as the kernels see it: clamped to the planned capacity (flagged).
+__device__ __forceinline__ int clamped_len(const int32_t* seq_lens, int b, const MainShape& sh,
+                                           uint32_t* status, bool report) {
   int seq = seq_lens[b];
   if (seq > sh.cap_tokens) {
-    if (split == 0 && kv == 0 && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_SEQ_TOO_LONG);
+    if (report) atomicOr(status, (uint32_t)MX_DEVICE_SEQ_TOO_LONG);
     seq = sh.cap_tokens;
   }
-  if (seq <= 0) {
-    // Empty sequence: defined as a zero output.
-    if (split == 0 && hvalid) {
-      uint16_t* op = out + ((int64_t)b * sh.num_heads + qhead) * D + (D / 4) * g4;
-#pragma unroll
-      for (int w = 0; w < D / 4; w += 8) *reinterpret_cast<u32x4*>(op + w) = u32x4{0, 0, 0, 0};
-    }
-    return;
-  }
-  const int t0 = split * sh.tokens_per_split;
-  if (t0 >= seq) return;
-  const int t1 = min(t0 + sh.tokens_per_split, seq);
-  const bool single = seq <= sh.tokens_per_split;
+  return seq;
+}
 
-  // Query operand: lane (h, g4) holds Q[h][32*i + 8*g4 .. +7] for MFMA i.
-  bf16x8 qop[D / 32];
-  {
-    const uint16_t* qp = q + ((int64_t)b * sh.num_heads + qhead) * D + 8 * g4;
+// Query operand of (b, kv): lane (h, g4) holds Q[kv*G + h][32*i + 8*g4 .. +7] for MFMA i.
+template <int D>
+__device__ __forceinline__ void load_q(bf16x8 (&qop)[D / 32], const uint16_t* q, int b, int kv,
+                                       const MainShape& sh, int lane) {
+  const int h = lane & 15;
+  const int g4 = lane >> 4;
+  const uint16_t* qp = q + ((int64_t)b * sh.num_heads + kv * sh.group + h) * D + 8 * g4;
 #pragma unroll
-    for (int i = 0; i < D / 32; ++i) {
-      u32x4 x = {0, 0, 0, 0};
-      if (hvalid) x = *reinterpret_cast<const u32x4*>(qp + 32 * i);
-      qop[i] = __builtin_bit_cast(bf16x8, x);
-    }
+  for (int i = 0; i < D / 32; ++i) {
+    u32x4 x = {0, 0, 0, 0};
+    if (h < sh.group) x = *reinterpret_cast<const u32x4*>(qp + 32 * i);
+    qop[i] = __builtin_bit_cast(bf16x8, x);
   }
+}
 
-  const int32_t* bt_row = block_table + (int64_t)b * sh.max_pages;
-  const int chunk_mask = (1 << sh.chunk_shift) - 1;
+// Streams chunks c_lo + wv + k*NW (k >= 0, < c_hi) of sequence b, KV head kv through this
+// wave's register ring, accumulating into `st`.  Chunk c_last is the sequence's last chunk and
+// holds `last_valid` tokens.
+template <int D, int NBUF, int NW>
+__device__ __forceinline__ void stream_chunks(SoftmaxState<D>& st, const bf16x8 (&qop)[D / 32],
+                                              const uint16_t* __restrict__ kc,
+                                              const uint16_t* __restrict__ vc,
+                                              const int32_t* __restrict__ bt_row, int kv,
+                                              int c_lo, int c_hi, int c_last, int last_valid,
+                                              int wv, char* klds, const MainShape& sh,
+                                              bool& bad_page) {
+  constexpr int VW = D / 16;
+  const int lane = threadIdx.x & 63;
+  const int r16 = lane & 15;
+  const int g4 = lane >> 4;
   LaneOffsets lo;
   lo.token_bytes = 2u * (uint32_t)sh.token_stride;
-  lo.k = 2u * (uint32_t)(r16 * sh.token_stride + kv * D + 8 * g4);
+  k_lane_offsets<D>(lo, lane, kv);
   lo.v = 2u * (uint32_t)(4 * g4 * sh.token_stride + kv * D + VW * r16);
-  bool bad_page = false;
+  const int chunk_mask = (1 << sh.chunk_shift) - 1;
+  const float sl2 = sh.scale_log2;
 
-  // Element offset of chunk c (16 tokens) of this sequence inside the K/V pools.  Only table
-  // entries below ceil(seq / page_size) are ever read.
+  // Element offset of chunk c (16 tokens) inside the K/V pools.  Only table entries below
+  // ceil(seq / page_size) are ever read.
   auto chunk_base = [&](int c) -> int64_t {
     int pid = bt_row[c >> sh.chunk_shift];
     if (pid < 0 || (sh.num_pages > 0 && pid >= sh.num_pages)) {
@@ -325,18 +423,9 @@ __global__ __launch_bounds__(64) void mx_paged_decode_splitkv(
     }
     return (int64_t)pid * sh.page_stride + (int64_t)((c & chunk_mask) * kChunk) * sh.token_stride;
   };
-
-  SoftmaxState<D> st;
-#pragma unroll
-  for (int i = 0; i < VW; ++i) st.o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  st.m = -INFINITY;
-  st.l = 0.f;
-
-  const int c0 = t0 / kChunk;
-  const int c1 = (t1 + kChunk - 1) / kChunk;    // chunk range [c0, c1), last may be partial
-  const int last_valid = t1 - (c1 - 1) * kChunk; // tokens of chunk c1-1 (1..16)
-  const float sl2 = sh.scale_log2;
-  auto nvalid_of = [&](int c) { return c == c1 - 1 ? last_valid : kChunk; };
+  const int n = (c_hi - c_lo > wv) ? (c_hi - c_lo - wv + NW - 1) / NW : 0;
+  auto gc = [&](int k) { return c_lo + wv + k * NW; };
+  auto nvalid_of = [&](int k) { return gc(k) == c_last ? last_valid : kChunk; };
 
   Chunk<D> buf[NBUF];
   auto load = [&](Chunk<D>& dst, int64_t base) { load_chunk<D>(dst, kc + base, vc + base, lo); };
@@ -344,85 +433,497 @@ __global__ __launch_bounds__(64) void mx_paged_decode_splitkv(
   // Register ring of NBUF chunks.  The steady-state loop processes NBUF full chunks and
   // refills their buffers with the next NBUF, with no conditional loads (so the compiler's
   // vmcnt waits stay partial); the page lookups of the refills are issued before the math.
-  const int n = c1 - c0;
   if (n >= NBUF) {
 #pragma unroll
-    for (int i = 0; i < NBUF; ++i) load(buf[i], chunk_base(c0 + i));
-    int c = c0;
-    while (c + 2 * NBUF <= c1) {
+    for (int i = 0; i < NBUF; ++i) load(buf[i], chunk_base(gc(i)));
+    int k = 0;
+    while (k + 2 * NBUF <= n) {
       int64_t nb[NBUF];
 #pragma unroll
-      for (int i = 0; i < NBUF; ++i) nb[i] = chunk_base(c + NBUF + i);
+      for (int i = 0; i < NBUF; ++i) nb[i] = chunk_base(gc(k + NBUF + i));
 #pragma unroll
       for (int i = 0; i < NBUF; ++i) {
-        process_chunk<D, false>(st, buf[i], qop, sl2, g4, kChunk);
+        process_chunk<D, false>(st, buf[i], qop, sl2, g4, kChunk, klds, lane);
         load(buf[i], nb[i]);
       }
-      c += NBUF;
+      k += NBUF;
     }
-    // c + NBUF <= c1 < c + 2*NBUF: buffers hold chunks c .. c+NBUF-1, `extra` more remain.
-    const int extra = c1 - c - NBUF;
+    // k + NBUF <= n < k + 2*NBUF: buffers hold chunks k .. k+NBUF-1, `extra` more remain.
+    const int extra = n - k - NBUF;
 #pragma unroll
     for (int i = 0; i < NBUF; ++i) {
       if (i < extra) {
-        const int64_t nbase = chunk_base(c + NBUF + i);
-        process_chunk<D, true>(st, buf[i], qop, sl2, g4, nvalid_of(c + i));
+        const int64_t nbase = chunk_base(gc(k + NBUF + i));
+        process_chunk<D, true>(st, buf[i], qop, sl2, g4, nvalid_of(k + i), klds, lane);
         load(buf[i], nbase);
       } else {
-        process_chunk<D, true>(st, buf[i], qop, sl2, g4, nvalid_of(c + i));
+        process_chunk<D, true>(st, buf[i], qop, sl2, g4, nvalid_of(k + i), klds, lane);
       }
     }
 #pragma unroll
     for (int i = 0; i < NBUF; ++i)
-      if (i < extra) process_chunk<D, true>(st, buf[i], qop, sl2, g4, nvalid_of(c + NBUF + i));
+      if (i < extra)
+        process_chunk<D, true>(st, buf[i], qop, sl2, g4, nvalid_of(k + NBUF + i), klds, lane);
   } else {
 #pragma unroll
     for (int i = 0; i < NBUF; ++i)
-      if (i < n) load(buf[i], chunk_base(c0 + i));
+      if (i < n) load(buf[i], chunk_base(gc(i)));
 #pragma unroll
     for (int i = 0; i < NBUF; ++i)
-      if (i < n) process_chunk<D, true>(st, buf[i], qop, sl2, g4, nvalid_of(c0 + i));
+      if (i < n) process_chunk<D, true>(st, buf[i], qop, sl2, g4, nvalid_of(i), klds, lane);
+  }
+}
+
+// Workgroup LDS: the per-wave K transpose tiles while streaming, then (after a barrier) the
+// per-wave softmax states for the merge.  Rows of s_o are padded by 4 floats so the 16 head
+// rows written by one store instruction fall in different banks.
+template <int D, int NW>
+struct GroupLds {
+  static constexpr int kRow = D + 4;
+  static constexpr int kKTile = k_via_lds<D>() ? 16 * 2 * D : 16;
+  static constexpr int kMergeBytes = NW * 16 * kRow * 4 + 2 * NW * 16 * 4;
+  static constexpr int kBytes = (NW * kKTile > kMergeBytes) ? NW * kKTile : kMergeBytes;
+  __device__ __forceinline__ static char* ktile(char* base, int wv) { return base + wv * kKTile; }
+  __device__ __forceinline__ static float* o(char* base) { return reinterpret_cast<float*>(base); }
+  __device__ __forceinline__ static float* m(char* base) { return o(base) + NW * 16 * kRow; }
+  __device__ __forceinline__ static float* l(char* base) { return m(base) + NW * 16; }
+};
+
+// Writes every wave's state to LDS (after a barrier that ends the K-tile use of the same
+// bytes) and synchronises, so merged_head() can combine them.
+template <int D, int NW>
+__device__ __forceinline__ void publish_wave_state(char* lds, const SoftmaxState<D>& st, int wv) {
+  using L = GroupLds<D, NW>;
+  constexpr int VW = D / 16;
+  const int lane = threadIdx.x & 63;
+  const int h = lane & 15;
+  const int g4 = lane >> 4;
+  const float l_w = group_sum4(st.l);
+  __syncthreads();
+  float* dst = L::o(lds) + (wv * 16 + h) * L::kRow + (D / 4) * g4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < VW; i += 4)
+      *reinterpret_cast<f32x4*>(dst + VW * j + i) =
+          f32x4{st.o[i][j], st.o[i + 1][j], st.o[i + 2][j], st.o[i + 3][j]};
+  if (g4 == 0) {
+    L::m(lds)[wv * 16 + h] = st.m;
+    L::l(lds)[wv * 16 + h] = l_w;
+  }
+  __syncthreads();
+}
+
+// Merged (normalised) dims d..d+3 of head slot hh and its log2-sum-exp.
+template <int D, int NW>
+__device__ __forceinline__ f32x4 merged_head(const char* lds, int hh, int d, float& lse) {
+  using L = GroupLds<D, NW>;
+  const float* sm = L::m(const_cast<char*>(lds));
+  const float* sl = L::l(const_cast<char*>(lds));
+  float mx = sm[hh];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) mx = fmaxf(mx, sm[w * 16 + hh]);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float lsum = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const float a = __builtin_amdgcn_exp2f(sm[w * 16 + hh] - mx);
+    lsum += a * sl[w * 16 + hh];
+    acc += a * *reinterpret_cast<const f32x4*>(L::o(const_cast<char*>(lds)) +
+                                              (w * 16 + hh) * L::kRow + d);
+  }
+  lse = mx + log2f(lsum);
+  return acc * (1.0f / lsum);
+}
+
+__device__ __forceinline__ void store_bf16x4(uint16_t* p, f32x4 v) {
+  const u32x2 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  *reinterpret_cast<u32x2*>(p) = w;
+}
+
+// ------------------------------------------------------------------------------------------
+// Split-grid kernel
+// ------------------------------------------------------------------------------------------
+
+// Grid (Hkv, batch, splits), NW waves per workgroup.  Consecutive workgroup ids, which the
+// dispatcher deals round-robin to the 8 XCDs, walk the KV heads of one sequence first, then
+// the sequences, then the splits.  Every XCD therefore gets an even share of the first split
+// of every sequence (where ragged batches keep most of their work), and the Hkv workgroups
+// that read the same physical pages start together.
+//
+// The NW waves of a workgroup share one (KV head, sequence, split): wave wv streams chunks
+// c0+wv, c0+wv+NW, ... through its own register ring (so NW times more K/V bytes are in flight
+// per split, with no global partials), and the waves merge their (m, l, O) states through LDS.
+template <int D, int NBUF, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
+    D == 64 ? MX_WAVES_PER_EU_D64 : (D == 128 ? MX_WAVES_PER_EU_D128 : MX_WAVES_PER_EU_D256))))
+void mx_paged_decode_splitkv(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, uint16_t* __restrict__ out,
+    const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ block_table,
+    float* __restrict__ part_o, float* __restrict__ part_lse, uint32_t* __restrict__ status,
+    const MainShape sh) {
+  using L = GroupLds<D, NW>;
+  __shared__ __attribute__((aligned(16))) char lds[L::kBytes];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  // Wave index, made provably wave-uniform so the chunk indices derived from it stay in
+  // SGPRs and the page lookups remain scalar loads (off the vector-memory counter).
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kv = blockIdx.x;
+  const int b = blockIdx.y;
+  const int split = blockIdx.z;
+  const int G = sh.group;
+  const int64_t row0 = (int64_t)b * sh.num_heads + kv * G;  // first query head row
+
+  const int seq = clamped_len(seq_lens, b, sh, status, split == 0 && kv == 0 && tid == 0);
+  if (seq <= 0) {
+    // Empty sequence: defined as a zero output.
+    if (split == 0)
+      for (int e = tid; e < G * (D / 4); e += 64 * NW)
+        store_bf16x4(out + (row0 + e / (D / 4)) * D + 4 * (e % (D / 4)), f32x4{0.f, 0.f, 0.f, 0.f});
+    return;
+  }
+  const int t0 = split * sh.tokens_per_split;
+  if (t0 >= seq) return;  // uniform over the workgroup: no barrier is skipped by part of it
+  const int t1 = min(t0 + sh.tokens_per_split, seq);
+  const bool single = seq <= sh.tokens_per_split;
+  const int n_chunks = (seq + kChunk - 1) / kChunk;
+
+  bf16x8 qop[D / 32];
+  load_q<D>(qop, q, b, kv, sh, lane);
+  SoftmaxState<D> st;
+#pragma unroll
+  for (int i = 0; i < D / 16; ++i) st.o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  st.m = -INFINITY;
+  st.l = 0.f;
+  bool bad_page = false;
+  stream_chunks<D, NBUF, NW>(st, qop, kc, vc, block_table + (int64_t)b * sh.max_pages, kv,
+                             t0 / kChunk, (t1 + kChunk - 1) / kChunk, n_chunks - 1,
+                             seq - (n_chunks - 1) * kChunk, wv, L::ktile(lds, wv), sh, bad_page);
+  if (bad_page && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
+  publish_wave_state<D, NW>(lds, st, wv);
+  for (int e = tid; e < G * (D / 4); e += 64 * NW) {
+    const int hh = e / (D / 4);
+    const int d = 4 * (e - hh * (D / 4));
+    float lse;
+    const f32x4 o = merged_head<D, NW>(lds, hh, d, lse);
+    const int64_t row = row0 + hh;
+    if (single) {
+      store_bf16x4(out + row * D + d, o);
+    } else {
+      *reinterpret_cast<f32x4*>(part_o + (row * sh.num_splits + split) * D + d) = o;
+      if (d == 0) part_lse[row * sh.num_splits + split] = lse;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Length-balanced kernel
+// ------------------------------------------------------------------------------------------
+
+constexpr int kMergeFanIn = 8;   // partials merged per step of the cross-workgroup merge tree
+constexpr int kMergeLevels = 4;  // enough for 8^4 = 4096 pieces per unit
+
+// Cross-workgroup handoff of partials.  Device-scoped accesses (MX_MERGE_SCOPED_ACCESS = 1):
+// partials are stored and loaded with agent-scope atomic accesses (write-through / coherent at
+// the device, sc1), each wave waits for its own stores to complete before the workgroup barrier
+// and the arrival counter; no L2 write-back or invalidate is needed.  Fenced (0): plain
+// accesses bracketed by __threadfence() in every thread (an L2 write-back per wave).
+#ifndef MX_MERGE_SCOPED_ACCESS
+#define MX_MERGE_SCOPED_ACCESS 1
+#endif
+
+__device__ __forceinline__ void store_partial4(float* p, f32x4 v) {
+#if MX_MERGE_SCOPED_ACCESS
+  const u32x4 u = __builtin_bit_cast(u32x4, v);
+  const uint64_t lo = (uint64_t)u[0] | ((uint64_t)u[1] << 32);
+  const uint64_t hi = (uint64_t)u[2] | ((uint64_t)u[3] << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p) + 1, hi, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+#else
+  *reinterpret_cast<f32x4*>(p) = v;
+#endif
+}
+__device__ __forceinline__ void store_partial1(float* p, float v) {
+#if MX_MERGE_SCOPED_ACCESS
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#else
+  *p = v;
+#endif
+}
+__device__ __forceinline__ f32x4 load_partial4(const float* p) {
+#if MX_MERGE_SCOPED_ACCESS
+  const uint64_t lo = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t hi = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p) + 1,
+                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const u32x4 u = {(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
+  return __builtin_bit_cast(f32x4, u);
+#else
+  return *reinterpret_cast<const f32x4*>(p);
+#endif
+}
+__device__ __forceinline__ float load_partial1(const float* p) {
+#if MX_MERGE_SCOPED_ACCESS
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#else
+  return *p;
+#endif
+}
+// Makes this thread's partial stores visible device-wide before the arrival count.
+__device__ __forceinline__ void publish_partials() {
+#if MX_MERGE_SCOPED_ACCESS
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);  // every store of this wave has completed
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+#else
+  __threadfence();
+#endif
+}
+// Orders the partial loads after the arrival count that proved them complete.
+__device__ __forceinline__ void acquire_partials() {
+#if MX_MERGE_SCOPED_ACCESS
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+#else
+  __threadfence();
+#endif
+}
+
+// Block-wide sum of one int per thread (all threads get the result).
+template <int NW>
+__device__ __forceinline__ int block_sum(int x, int* sred) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sred[threadIdx.x >> 6] = x;
+  __syncthreads();
+  int t = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) t += sred[w];
+  return t;
+}
+
+// One launch of num_groups workgroups covers the whole batch whatever the length mix.  Every
+// (sequence b, KV head kv) "unit" with n_b = ceil(L_b/16) > 0 chunks occupies n_b +
+// unit_overhead consecutive positions of one global line (units in (b, kv) order; the
+// overhead charges the per-unit Q load and pipeline fill); workgroup w owns positions
+// [w*q, (w+1)*q) with q = ceil(total / num_groups), found from seq_lens on the device, so a
+// ragged batch is balanced without the host seeing its lengths.  A unit a workgroup covers
+// entirely is written out as bf16; a unit cut into several pieces has each piece written as
+// a normalised partial (O/l, log2-sum-exp) to its own slot, and the last piece to finish
+// merges them through a fan-in-8 tree of per-unit counters, so the whole call is one launch.
+template <int D, int NBUF, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
+    D == 64 ? MX_WAVES_PER_EU_D64 : (D == 128 ? MX_WAVES_PER_EU_D128 : MX_WAVES_PER_EU_D256))))
+void mx_paged_decode_balanced(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, uint16_t* __restrict__ out,
+    const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ block_table,
+    float* __restrict__ part_o, float* __restrict__ part_lse, uint32_t* __restrict__ counters,
+    uint32_t* __restrict__ status, const MainShape sh) {
+  using L = GroupLds<D, NW>;
+  __shared__ __attribute__((aligned(16))) char lds[L::kBytes];
+  __shared__ int s_int[NW + 4];
+  __shared__ float s_lse[16];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wg = blockIdx.x;
+  const int G = sh.group;
+  const int Hkv = sh.num_kv_heads;
+  const int B = sh.batch;
+  const int alpha = sh.unit_overhead;
+
+  // Empty sequences (L <= 0) are defined as zero output; sequence b's zeros are written by
+  // workgroup b % num_groups.
+  for (int b = wg; b < B; b += sh.num_groups) {
+    if (seq_lens[b] <= 0)
+      for (int e = tid; e < sh.num_heads * (D / 4); e += 64 * NW)
+        store_bf16x4(out + ((int64_t)b * sh.num_heads + e / (D / 4)) * D + 4 * (e % (D / 4)),
+                     f32x4{0.f, 0.f, 0.f, 0.f});
   }
 
-  if (bad_page && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
+  // Pass 1: total positions.
+  auto weight = [&](int b, bool report) -> int {
+    const int seq = clamped_len(seq_lens, b, sh, status, report);
+    return seq > 0 ? Hkv * ((seq + kChunk - 1) / kChunk + alpha) : 0;
+  };
+  int total = 0;
+  for (int base = 0; base < B; base += 64 * NW) {
+    const int b = base + tid;
+    total += block_sum<NW>(b < B ? weight(b, wg == 0) : 0, s_int);
+  }
+  if (total == 0) return;
+  const int qsz = (total + sh.num_groups - 1) / sh.num_groups;
+  const int x_begin = wg * qsz;
+  if (x_begin >= total) return;
+  const int x_end = min(x_begin + qsz, total);
 
-  const float l_tot = group_sum4(st.l);
-  const float inv = 1.0f / l_tot;
-  if (!hvalid) return;
-  const int64_t row = (int64_t)b * sh.num_heads + qhead;
-  if (single) {
-    // bf16 output: lane writes dims [D/4*g4, D/4*(g4+1)), element VW*j + i = o[i][j].
-    uint16_t* op = out + row * D + (D / 4) * g4;
+  // Pass 2: the sequence holding position x_begin and the position where it starts.
+  if (tid == 0) s_int[NW] = -1;
+  int carry = 0;
+  for (int base = 0; base < B; base += 64 * NW) {
+    const int b = base + tid;
+    const int w = b < B ? weight(b, false) : 0;
+    int incl = w;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if constexpr (VW == 4) {
-        const u32x2 w = {pack_bf16x2(st.o[0][j] * inv, st.o[1][j] * inv),
-                         pack_bf16x2(st.o[2][j] * inv, st.o[3][j] * inv)};
-        *reinterpret_cast<u32x2*>(op + VW * j) = w;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(incl, off);
+      if (lane >= off) incl += y;
+    }
+    __syncthreads();
+    if (lane == 63) s_int[wv] = incl;
+    __syncthreads();
+    int before = carry;
+    for (int w2 = 0; w2 < wv; ++w2) before += s_int[w2];
+    const int start = before + incl - w;
+    if (w > 0 && start <= x_begin && x_begin < start + w) {
+      s_int[NW] = b;
+      s_int[NW + 1] = start;
+    }
+    int blk = 0;
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2) blk += s_int[w2];
+    carry += blk;
+    __syncthreads();
+    if (carry > x_begin) break;  // uniform: every thread holds the same carry
+  }
+  int b = __builtin_amdgcn_readfirstlane(s_int[NW]);
+  int seq_start = __builtin_amdgcn_readfirstlane(s_int[NW + 1]);
+  if (b < 0) return;  // unreachable: the positions of non-empty sequences tile [0, total)
+
+  int seq = clamped_len(seq_lens, b, sh, status, false);
+  int n_b = (seq + kChunk - 1) / kChunk;
+  int span = n_b + alpha;
+  int j = (x_begin - seq_start) / span;  // head slot of the unit in position order
+  int u0 = seq_start + j * span;  // first position of unit (b, j)
+  const int per_level = kMaxSlots;  // counters of merge level l start at l * kMaxSlots
+  bool bad_page = false;
+
+  for (;;) {
+    // Unit (b, j): positions [u0, u0 + span), its chunk c at position u0 + alpha + c.
+    const int cpos = u0 + alpha;
+    const int ca = max(x_begin, cpos) - cpos;
+    const int cb = min(x_end, cpos + n_b) - cpos;
+    if (ca < cb) {
+      const int unit = b * Hkv + j;
+      const int kv = j;
+      const int first_wg = cpos / qsz;
+      const int npieces = (cpos + n_b - 1) / qsz - first_wg + 1;
+      const int64_t row0 = (int64_t)b * sh.num_heads + kv * G;
+
+      bf16x8 qop[D / 32];
+      load_q<D>(qop, q, b, kv, sh, lane);
+      SoftmaxState<D> st;
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) st.o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      st.m = -INFINITY;
+      st.l = 0.f;
+      stream_chunks<D, NBUF, NW>(st, qop, kc, vc, block_table + (int64_t)b * sh.max_pages, kv,
+                                 ca, cb, n_b - 1, seq - (n_b - 1) * kChunk, wv,
+                                 L::ktile(lds, wv), sh, bad_page);
+      publish_wave_state<D, NW>(lds, st, wv);
+
+      if (npieces == 1) {
+        for (int e = tid; e < G * (D / 4); e += 64 * NW) {
+          const int hh = e / (D / 4);
+          const int d = 4 * (e - hh * (D / 4));
+          float lse;
+          store_bf16x4(out + (row0 + hh) * D + d, merged_head<D, NW>(lds, hh, d, lse));
+        }
       } else {
+        // Piece k of the unit goes to slot slot0 + k; level-l item j of the merge tree covers
+        // pieces [j*8^l, (j+1)*8^l) and lives in the slot of its first piece.
+        const int slot0 = first_wg + unit;
+        int item = wg - first_wg;
+        {
+          float* po = part_o + (int64_t)(slot0 + item) * G * D;
+          float* pl = part_lse + (int64_t)(slot0 + item) * G;
+          for (int e = tid; e < G * (D / 4); e += 64 * NW) {
+            const int hh = e / (D / 4);
+            const int d = 4 * (e - hh * (D / 4));
+            float lse;
+            store_partial4(po + hh * D + d, merged_head<D, NW>(lds, hh, d, lse));
+            if (d == 0) store_partial1(pl + hh, lse);
+          }
+        }
+        int nitems = npieces;
+        int stride = 1;  // pieces per item at this level
+        for (int level = 0; level < kMergeLevels; ++level) {
+          const int grp = item / kMergeFanIn;
+          const int gsize = min(kMergeFanIn, nitems - grp * kMergeFanIn);
+          const int gslot = slot0 + grp * kMergeFanIn * stride;
+          // Publish this workgroup's stores device-wide, then count arrivals of the group.
+          publish_partials();
+          __syncthreads();
+          if (tid == 0) {
+            const uint32_t prev = atomicAdd(&counters[level * per_level + gslot], 1u);
+            s_int[NW + 2] = (prev == (uint32_t)(gsize - 1)) ? 1 : 0;
+          }
+          __syncthreads();
+          if (!s_int[NW + 2]) break;  // another piece of the group is still running
+          if (tid == 0) counters[level * per_level + gslot] = 0u;  // ready for the next call
+          acquire_partials();
+          const int nnext = (nitems + kMergeFanIn - 1) / kMergeFanIn;
+          // Merge items grp*8 .. grp*8+gsize-1 (slots gslot + t*stride).
+          for (int e = tid; e < G * (D / 4); e += 64 * NW) {
+            const int hh = e / (D / 4);
+            const int d = 4 * (e - hh * (D / 4));
+            float mx = -INFINITY;
+            float lses[kMergeFanIn];
 #pragma unroll
-        for (int i = 0; i < VW; i += 8) {
-          u32x4 w;
+            for (int t = 0; t < kMergeFanIn; ++t) {
+              lses[t] = t < gsize ? load_partial1(part_lse + (int64_t)(gslot + t * stride) * G + hh)
+                                  : -INFINITY;
+              mx = fmaxf(mx, lses[t]);
+            }
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            float wsum = 0.f;
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            w[e] = pack_bf16x2(st.o[i + 2 * e][j] * inv, st.o[i + 2 * e + 1][j] * inv);
-          *reinterpret_cast<u32x4*>(op + VW * j + i) = w;
+            for (int t = 0; t < kMergeFanIn; ++t) {
+              if (t < gsize) {
+                const int64_t sl = gslot + t * stride;
+                const float w = __builtin_amdgcn_exp2f(lses[t] - mx);
+                wsum += w;
+                acc += w * load_partial4(part_o + (sl * G + hh) * D + d);
+              }
+            }
+            acc *= 1.0f / wsum;
+            if (nnext == 1) {
+              store_bf16x4(out + (row0 + hh) * D + d, acc);
+            } else {
+              store_partial4(part_o + ((int64_t)gslot * G + hh) * D + d, acc);
+              if (d == 0) s_lse[hh] = mx + log2f(wsum);
+            }
+          }
+          if (nnext == 1) break;
+          // Every thread has read the group's log-sum-exps before any is overwritten.
+          __syncthreads();
+          if (tid < G) store_partial1(part_lse + (int64_t)gslot * G + tid, s_lse[tid]);
+          item = grp;
+          nitems = nnext;
+          stride *= kMergeFanIn;
         }
       }
+      // The merged states in LDS share bytes with the K tiles the next piece streams into:
+      // no wave may start that piece until every wave has finished reading them.
+      __syncthreads();
     }
-  } else {
-    float* pp = part_o + (row * sh.num_splits + split) * D + (D / 4) * g4;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int i = 0; i < VW; i += 4) {
-        const f32x4 w = {st.o[i][j] * inv, st.o[i + 1][j] * inv, st.o[i + 2][j] * inv,
-                         st.o[i + 3][j] * inv};
-        *reinterpret_cast<f32x4*>(pp + VW * j + i) = w;
-      }
+    // Next unit.
+    u0 += span;
+    if (u0 >= x_end) break;
+    if (++j == Hkv) {
+      j = 0;
+      seq = 0;
+      while (seq <= 0 && ++b < B) seq = clamped_len(seq_lens, b, sh, status, false);
+      if (b >= B) break;  // unreachable: positions only exist for non-empty sequences
+      n_b = (seq + kChunk - 1) / kChunk;
+      span = n_b + alpha;
     }
-    if (g4 == 0) part_lse[row * sh.num_splits + split] = st.m + log2f(l_tot);
   }
+  if (bad_page && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -507,22 +1008,40 @@ int ok() {
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int64_t align_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 
-// Split policy (replaces the 104-SM regime table of submission_clean.cu:375-430).  Measured
-// on MI355X: the split-KV kernel reaches the device's streaming-read ceiling once about
-// 8 MB of K/V loads are in flight, i.e. 2 single-wave workgroups per CU for D=128 (8 KB per
-// 16-token chunk, 2 chunks in flight per wave) and 4 per CU for D=64 (4 KB chunks) and
-// D=256 (one wave per SIMD, issue-bound).  Every extra split costs a wave prologue and a
-// partial write, so the policy asks for just enough splits to reach that wave count.
+// Schedule policy (replaces the 104-SM regime table of submission_clean.cu:375-430), from
+// interleaved A/B sweeps on MI355X over the five north-star configurations:
+//  * workgroups per CU: one cooperative 4-wave group for D=128 and D=256, two 2-wave groups
+//    for D=64 -- more resident groups contend for HBM without adding bandwidth;
+//  * batches with at least kBalancedMinUnits (sequence, KV head) units take the balanced
+//    single launch (lengths balanced on the device, ~84% of 8 TB/s on Llama-3-8B decode);
+//  * fewer, long units (long-context decode) take the split grid, whose page-aligned splits
+//    plus a separate combine beat the balanced merge tree by ~10% there;
+//  * split counts: just enough splits for the workgroup target, each at least
+//    kMinTokensPerSplit long and at most kMaxTokensPerSplit.
 constexpr int64_t kMinTokensPerSplit = 128;   // amortises Q load, pipeline fill and partials
-constexpr int64_t kMaxTokensPerSplit = 4096;  // bounds one wave's share of a long sequence
+constexpr int64_t kMaxTokensPerSplit = 16384;  // bounds one workgroup's share of a sequence
 constexpr int64_t kMaxGridDim = 65535;
+constexpr int64_t kBalancedMinUnits = 64;
 
-int64_t target_waves_per_cu(int64_t head_dim) { return head_dim == 128 ? 2 : 4; }
+int64_t groups_per_cu(int64_t head_dim) { return head_dim == 64 ? 2 : 1; }
+
+// Balanced schedule limits: the largest batch whose seq_lens scan stays within two passes of
+// one workgroup; the per-unit overhead (chunk positions) is MX_UNIT_OVERHEAD.
+#ifndef MX_UNIT_OVERHEAD
+#define MX_UNIT_OVERHEAD 6
+#endif
+constexpr int64_t kBalancedMaxBatch = 512;
+constexpr int64_t kBalancedMaxGroups = 4095;  // pieces per unit stay within the 8^4 merge tree
+constexpr int64_t kBalancedMaxUnits = 8192;   // batch * Hkv (fixed counter region)
 
 struct Plan {
-  int64_t splits = 1;
-  int64_t tokens_per_split = 0;
+  int schedule = MX_SCHEDULE_SPLIT_GRID;
+  int64_t splits = 1;             // split grid: splits per sequence
+  int64_t tokens_per_split = 0;   // split grid
+  int64_t groups = 0;             // balanced: workgroups of the launch
+  int64_t slots = 0;              // balanced: partial slots (groups + batch * Hkv)
   int64_t cap_tokens = 0;
+  int64_t counter_offset = 0;
   int64_t lse_offset = 0;
   int64_t o_offset = 0;
   int64_t workspace_bytes = kStatusBytes;
@@ -570,7 +1089,6 @@ int make_plan(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t he
   if (page_size != 16 && page_size != 32 && page_size != 64 && page_size != 128 &&
       page_size != 256)
     return fail(MX_STATUS_UNSUPPORTED, "page_size must be 16, 32, 64, 128 or 256");
-  if (num_splits < 0) return fail(MX_STATUS_INVALID_SHAPE, "num_splits must be >= 0");
   if (batch > kMaxGridDim) return fail(MX_STATUS_UNSUPPORTED, "batch must be <= 65535");
   if (num_heads > kMaxGridDim) return fail(MX_STATUS_UNSUPPORTED, "num_heads must be <= 65535");
   if (max_pages > (int64_t)INT32_MAX / page_size)
@@ -584,13 +1102,15 @@ int make_plan(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t he
   int64_t ns;
   if (num_splits > 0) {
     ns = num_splits;
+  } else if (num_splits < 0) {
+    ns = 1;
   } else {
     if (num_cus <= 0) {
       const int st = query_num_cus(&num_cus);
       if (st != MX_STATUS_OK) return st;
     }
     const int64_t units = batch * num_kv_heads;
-    ns = ceil_div(num_cus * target_waves_per_cu(head_dim), units);
+    ns = ceil_div(num_cus * groups_per_cu(head_dim), units);
     const int64_t max_by_len = ceil_div(cap, kMinTokensPerSplit);
     if (ns > max_by_len) ns = max_by_len;
     const int64_t min_by_len = ceil_div(cap, kMaxTokensPerSplit);
@@ -608,10 +1128,41 @@ int make_plan(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t he
   int shift = 0;
   while ((int64_t(kChunk) << shift) < page_size) ++shift;
   plan->chunk_shift = shift;
+  const bool balanced_ok = batch <= kBalancedMaxBatch && batch * num_kv_heads <= kBalancedMaxUnits;
+  const bool balanced_auto = num_splits == 0 && balanced_ok && batch * num_kv_heads >= kBalancedMinUnits;
+  if ((num_splits < 0 && balanced_ok) || balanced_auto) {
+    // Length-balanced single launch (automatic, or num_splits < 0 = that many workgroups).
+    int64_t groups;
+    if (num_splits < 0) {
+      groups = -num_splits;
+    } else {
+      if (num_cus <= 0) {
+        const int st = query_num_cus(&num_cus);
+        if (st != MX_STATUS_OK) return st;
+      }
+      groups = num_cus * groups_per_cu(head_dim);
+    }
+    if (groups > kBalancedMaxGroups) groups = kBalancedMaxGroups;
+    const int64_t group = num_heads / num_kv_heads;
+    plan->schedule = MX_SCHEDULE_BALANCED;
+    plan->splits = 0;
+    plan->tokens_per_split = 0;
+    plan->groups = groups;
+    plan->slots = groups + batch * num_kv_heads;
+    plan->cap_tokens = cap;
+    plan->counter_offset = kStatusBytes;
+    plan->lse_offset = kPartialBase;
+    plan->o_offset = plan->lse_offset + align_up(plan->slots * group * 4, 256);
+    plan->workspace_bytes = plan->o_offset + plan->slots * group * head_dim * 4;
+    return MX_STATUS_OK;
+  }
+  if (num_splits < 0)
+    return fail(MX_STATUS_UNSUPPORTED,
+                "the balanced schedule supports batch <= 512 and batch * num_kv_heads <= 8192");
   if (ns > 1) {
     const int64_t rows = batch * num_heads * ns;
-    plan->lse_offset = kStatusBytes;
-    plan->o_offset = kStatusBytes + align_up(rows * 4, 256);
+    plan->lse_offset = kPartialBase;
+    plan->o_offset = kPartialBase + align_up(rows * 4, 256);
     plan->workspace_bytes = plan->o_offset + rows * head_dim * 4;
   } else {
     plan->lse_offset = plan->o_offset = 0;
@@ -650,7 +1201,8 @@ int internal_workspace(int64_t need, void** out) {
       (void)hipGetLastError();
       return fail(MX_STATUS_ALLOC_FAILED, "hipMalloc of the internal workspace failed");
     }
-    if (hipMemset(p, 0, kStatusBytes) != hipSuccess) {
+    // status word and merge counters must start at zero
+    if (hipMemset(p, 0, (size_t)std::min<int64_t>(bytes, kPartialBase)) != hipSuccess) {
       (void)hipGetLastError();
       (void)hipFree(p);
       return fail(MX_STATUS_HIP_ERROR, "hipMemset of the internal workspace failed");
@@ -667,26 +1219,48 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
                   const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
                   int64_t num_heads, int64_t num_kv_heads, int64_t page_size, int64_t num_pages,
                   int64_t max_pages, float scale, char* ws, int32_t phase, hipStream_t stream) {
+  constexpr int kNW = waves_per_group<D>();
+  constexpr int kNBUF = ring_depth<D>();
+  MainShape sh;
+  sh.page_stride = page_size * num_kv_heads * D;
+  sh.token_stride = (int)(num_kv_heads * D);
+  sh.num_heads = (int)num_heads;
+  sh.num_kv_heads = (int)num_kv_heads;
+  sh.group = (int)(num_heads / num_kv_heads);
+  sh.batch = (int)batch;
+  sh.max_pages = (int)max_pages;
+  sh.num_pages = (num_pages > 0 && num_pages <= INT32_MAX) ? (int)num_pages : 0;
+  sh.chunk_shift = plan.chunk_shift;
+  sh.cap_tokens = (int)plan.cap_tokens;
+  sh.scale_log2 = scale * 1.4426950408889634f;
+  sh.num_splits = (int)plan.splits;
+  sh.tokens_per_split = (int)plan.tokens_per_split;
+  sh.num_groups = (int)plan.groups;
+  sh.unit_overhead = MX_UNIT_OVERHEAD;
+  sh.num_slots = (int)plan.slots;
+  uint32_t* status = reinterpret_cast<uint32_t*>(ws);
+
+  if (plan.schedule == MX_SCHEDULE_BALANCED) {
+    // One launch does everything; MX_PHASE_COMBINE_ONLY has nothing left to do.
+    if (phase == MX_PHASE_COMBINE_ONLY) return hipSuccess;
+    hipLaunchKernelGGL((mx_paged_decode_balanced<D, kNBUF, kNW>), dim3((unsigned)plan.groups),
+                       dim3(64 * kNW), 0, stream, static_cast<const uint16_t*>(q),
+                       static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+                       static_cast<uint16_t*>(out), seq_lens, block_table,
+                       reinterpret_cast<float*>(ws + plan.o_offset),
+                       reinterpret_cast<float*>(ws + plan.lse_offset),
+                       reinterpret_cast<uint32_t*>(ws + plan.counter_offset), status, sh);
+    return hipGetLastError();
+  }
+
   float* part_lse = plan.splits > 1 ? reinterpret_cast<float*>(ws + plan.lse_offset) : nullptr;
   float* part_o = plan.splits > 1 ? reinterpret_cast<float*>(ws + plan.o_offset) : nullptr;
   if (phase != MX_PHASE_COMBINE_ONLY) {
-    MainShape sh;
-    sh.page_stride = page_size * num_kv_heads * D;
-    sh.token_stride = (int)(num_kv_heads * D);
-    sh.num_heads = (int)num_heads;
-    sh.group = (int)(num_heads / num_kv_heads);
-    sh.max_pages = (int)max_pages;
-    sh.num_pages = (num_pages > 0 && num_pages <= INT32_MAX) ? (int)num_pages : 0;
-    sh.chunk_shift = plan.chunk_shift;
-    sh.num_splits = (int)plan.splits;
-    sh.tokens_per_split = (int)plan.tokens_per_split;
-    sh.cap_tokens = (int)plan.cap_tokens;
-    sh.scale_log2 = scale * 1.4426950408889634f;
     const dim3 grid((unsigned)num_kv_heads, (unsigned)batch, (unsigned)plan.splits);
-    hipLaunchKernelGGL((mx_paged_decode_splitkv<D, ring_depth<D>()>), grid, dim3(64), 0, stream,
-                       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+    hipLaunchKernelGGL((mx_paged_decode_splitkv<D, kNBUF, kNW>), grid, dim3(64 * kNW), 0,
+                       stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                        static_cast<const uint16_t*>(v), static_cast<uint16_t*>(out), seq_lens,
-                       block_table, part_o, part_lse, reinterpret_cast<uint32_t*>(ws), sh);
+                       block_table, part_o, part_lse, status, sh);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -712,14 +1286,19 @@ extern "C" {
 int mx_paged_gqa_decode_plan(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
                              int64_t head_dim, int64_t page_size, int64_t max_pages_per_seq,
                              int64_t max_seq_len, int64_t num_splits, int64_t num_cus,
-                             int64_t* splits_out, int64_t* tokens_per_split_out,
+                             int64_t* schedule_out, int64_t* splits_out,
+                             int64_t* tokens_per_split_out, int64_t* workgroups_out,
                              int64_t* workspace_bytes_out) {
   Plan plan;
   const int st = make_plan(batch, num_heads, num_kv_heads, head_dim, page_size,
                            max_pages_per_seq, max_seq_len, num_splits, num_cus, &plan);
   if (st != MX_STATUS_OK) return st;
+  if (schedule_out) *schedule_out = plan.schedule;
   if (splits_out) *splits_out = plan.splits;
   if (tokens_per_split_out) *tokens_per_split_out = plan.tokens_per_split;
+  if (workgroups_out)
+    *workgroups_out = plan.schedule == MX_SCHEDULE_BALANCED ? plan.groups
+                                                            : batch * num_kv_heads * plan.splits;
   if (workspace_bytes_out) *workspace_bytes_out = plan.workspace_bytes;
   return ok();
 }

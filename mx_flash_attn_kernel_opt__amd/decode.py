@@ -37,16 +37,20 @@ def plan(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, page_size
          num_cus: int = 0) -> dict:
     """Split plan of a call (host only when ``num_cus`` > 0).
 
-    Returns ``{"splits", "tokens_per_split", "workspace_bytes"}``; raises MXAttnError for an
-    invalid or unsupported shape.
+    Returns ``{"schedule", "splits", "tokens_per_split", "workgroups", "workspace_bytes"}``
+    (schedule: "split_grid" or "balanced"); raises MXAttnError for an invalid or unsupported
+    shape.
     """
     lib = _lib.load()
-    ns, tps, ws = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    sch, ns, tps, wgs, ws = (ctypes.c_int64() for _ in range(5))
     st = lib.mx_paged_gqa_decode_plan(batch, num_heads, num_kv_heads, head_dim, page_size,
                                       max_pages_per_seq, max_seq_len, num_splits, num_cus,
-                                      ctypes.byref(ns), ctypes.byref(tps), ctypes.byref(ws))
+                                      ctypes.byref(sch), ctypes.byref(ns), ctypes.byref(tps),
+                                      ctypes.byref(wgs), ctypes.byref(ws))
     _lib.check(st)
-    return {"splits": ns.value, "tokens_per_split": tps.value, "workspace_bytes": ws.value}
+    return {"schedule": "balanced" if sch.value == _lib.MX_SCHEDULE_BALANCED else "split_grid",
+            "splits": ns.value, "tokens_per_split": tps.value, "workgroups": wgs.value,
+            "workspace_bytes": ws.value}
 
 
 def workspace_size(batch: int, num_heads: int, num_kv_heads: int, head_dim: int,

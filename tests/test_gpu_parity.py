@@ -260,3 +260,106 @@ def test_golden_task_example_through_run_kernel():
                B, 512, 1, 32, 4, 128, 16, B * W_, 0)
     torch.cuda.synchronize()
     assert_close_to_oracle(out, expected, "task_example run_kernel")
+
+
+# ------------------------------------------------------------------------------------------
+# Length-balanced single-launch schedule (num_splits < 0 forces its workgroup count)
+# ------------------------------------------------------------------------------------------
+
+RAGGED_LENS = [1, 15, 16, 17, 100, 1000, 4096, 33, 2, 777, 63, 64, 65, 3000]
+
+
+@pytest.mark.parametrize("groups", [1, 3, 8, 64, 512, 2000])
+@pytest.mark.parametrize("D,Hq,Hkv,P", [(128, 28, 4, 64), (64, 32, 4, 16), (256, 16, 2, 16)])
+def test_balanced_any_workgroup_count(groups, D, Hq, Hkv, P):
+    spec = W.custom_spec(f"bal_D{D}", RAGGED_LENS, Hq, Hkv, D, P)
+    inp = W.make_inputs(spec, seed=groups + D, device=DEV)
+    out = _decode(inp, num_splits=-groups)
+    _check(inp, out, label=f"balanced groups={groups} D={D}")
+    assert read_device_status() == 0
+
+
+def test_balanced_repeated_calls_are_identical():
+    """Per-unit merge counters reset themselves: back-to-back calls (many pieces per unit, a
+    two-level merge tree) give bitwise-identical results."""
+    inp = W.make_inputs("long_b1_32k", seed=11, device=DEV)
+    ws = torch.zeros(1 << 24, dtype=torch.uint8, device=DEV)
+    outs = [_decode(inp, num_splits=-512, workspace=ws).clone() for _ in range(3)]
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
+    _check(inp, outs[0], label="long_b1_32k balanced")
+    assert read_device_status(ws) == 0
+
+
+def test_balanced_deep_merge_tree():
+    """One unit cut into ~4000 pieces: a four-level fan-in-8 merge."""
+    spec = W.custom_spec("deep", [70000], 8, 1, 64, 16)
+    inp = W.make_inputs(spec, seed=12, device=DEV)
+    out = _decode(inp, num_splits=-4095)
+    _check(inp, out, label="deep merge")
+    out2 = _decode(inp, num_splits=-4095)
+    assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("groups", [0, -1, -5, -100])
+def test_balanced_empty_sequences(groups):
+    spec = W.custom_spec("empty_bal", [0, 5, 0, 300, 0, 1], 32, 8, 128, 16, max_pages=20)
+    inp = W.make_inputs(spec, seed=13, device=DEV)
+    inp.seq_lens.copy_(torch.tensor([0, 5, 0, 300, 0, 1], dtype=torch.int32, device=DEV))
+    out = _decode(inp, num_splits=groups)
+    for b in (0, 2, 4):
+        assert torch.count_nonzero(out[b]).item() == 0
+    _check(inp, out, batches=[1, 3, 5], label=f"empty groups={groups}")
+
+
+def test_balanced_matches_split_grid():
+    inp = W.make_inputs("ragged", seed=14, device=DEV)
+    a = _decode(inp, num_splits=0)
+    b = _decode(inp, num_splits=8)
+    assert (a.float() - b.float()).abs().max().item() <= 1e-2
+    _check(inp, a, _sample(inp.spec.batch, 40), label="ragged balanced")
+
+
+# ------------------------------------------------------------------------------------------
+# Device-side bounds checks (the kernels' own checks turn bad input into a status bit)
+# ------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("ns", [0, 2])
+def test_bad_page_id_is_flagged_not_read(ns):
+    spec = W.custom_spec("badpage", [40, 70], 32, 8, 128, 16, max_pages=5, pool_pages=16)
+    inp = W.make_inputs(spec, seed=15, device=DEV)
+    ws = torch.zeros(1 << 22, dtype=torch.uint8, device=DEV)
+    bt = inp.block_table.clone()
+    bt[1, 2] = spec.num_pages + 7          # a valid slot (70 tokens use 5 pages) out of the pool
+    out = paged_gqa_decode(inp.q, inp.k_cache, inp.v_cache, bt, inp.seq_lens, inp.scale,
+                           num_splits=ns, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    assert read_device_status(ws) & 1      # MX_DEVICE_BAD_PAGE_ID
+    assert read_device_status(ws) == 0     # the read above cleared it
+    _check(inp, out, batches=[0], label="unaffected sequence")
+
+
+@pytest.mark.parametrize("ns", [0, 1])
+def test_sequence_longer_than_planned_capacity_is_flagged(ns):
+    spec = W.custom_spec("toolong", [100, 500], 32, 8, 128, 16, max_pages=32)
+    inp = W.make_inputs(spec, seed=16, device=DEV)
+    ws = torch.zeros(1 << 22, dtype=torch.uint8, device=DEV)
+    out = paged_gqa_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_table, inp.seq_lens,
+                           inp.scale, num_splits=ns, max_seq_len=200, workspace=ws)
+    torch.cuda.synchronize()
+    assert read_device_status(ws) & 2      # MX_DEVICE_SEQ_TOO_LONG
+    assert torch.isfinite(out.float()).all()
+    _check(inp, out, batches=[0], label="in-capacity sequence")
+
+
+def test_library_workspace_survives_schedule_and_shape_changes():
+    """Regression: the library-owned workspace must present zeroed merge counters to every
+    balanced call, after split-grid calls wrote partials and after the workspace grew."""
+    seq = [("tiny", 4), ("long_b1_32k", 0), ("tiny", 0), ("long_b4_32k", 16), ("long_b1_32k", 0),
+           ("ragged", 3), ("ragged", 0), ("long_b1_32k", -700)]
+    for name, ns in seq:
+        inp = W.make_inputs(name, seed=17, device=DEV)
+        out = _decode(inp, num_splits=ns)
+        _check(inp, out, _sample(inp.spec.batch, 8), label=f"{name} ns={ns}")
+        assert read_device_status() == 0
+        del inp

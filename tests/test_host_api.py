@@ -64,6 +64,7 @@ def test_run_kernel_abi_matches_the_reference_binding():
 # ------------------------------------------------------------------------------------------
 
 FAKE = ctypes.c_void_p(0x1000)   # never dereferenced: validation fails first
+PARTIAL_BASE = 256 + 4 * (4096 + 8192) * 4   # status word + fixed merge-counter region
 
 
 def _decode(**over):
@@ -91,7 +92,8 @@ def test_null_pointers_are_rejected(field):
     (dict(Hkv=0), _lib.MX_STATUS_INVALID_SHAPE),
     (dict(max_pages=0), _lib.MX_STATUS_INVALID_SHAPE),
     (dict(pages=-1), _lib.MX_STATUS_INVALID_SHAPE),
-    (dict(ns=-3), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(ns=-3, B=600), _lib.MX_STATUS_UNSUPPORTED),     # balanced schedule: batch <= 512
+    (dict(ns=-3, B=500, Hq=32, Hkv=32), _lib.MX_STATUS_UNSUPPORTED),   # batch * Hkv <= 8192
     (dict(D=96), _lib.MX_STATUS_UNSUPPORTED),
     (dict(D=512), _lib.MX_STATUS_UNSUPPORTED),
     (dict(P=8), _lib.MX_STATUS_UNSUPPORTED),
@@ -148,17 +150,19 @@ def test_python_wrapper_raises_with_status():
 # ------------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("B,Hq,Hkv,D,P,max_pages,cap,ns_req", [
-    (64, 32, 8, 128, 16, 256, 0, 0),
-    (1, 64, 8, 128, 16, 8192, 0, 0),
-    (256, 28, 4, 128, 64, 128, 0, 0),
-    (4, 32, 8, 128, 16, 32, 512, 0),
-    (3, 32, 8, 128, 16, 40, 300, 0),
+    (64, 32, 8, 128, 16, 256, 0, 3),
+    (1, 64, 8, 128, 16, 8192, 0, 64),
+    (256, 28, 4, 128, 64, 128, 0, 5),
+    (4, 32, 8, 128, 16, 32, 512, 2),
+    (3, 32, 8, 128, 16, 40, 300, 7),
     (8, 32, 8, 64, 32, 100, 0, 7),
     (2, 16, 2, 256, 16, 10, 0, 1000),
-    (1, 32, 4, 128, 16, 1, 1, 0),
+    (1, 32, 4, 128, 16, 1, 1, 1),
+    (600, 32, 8, 128, 16, 64, 0, 0),      # automatic plan above the balanced batch limit
 ])
-def test_plan_invariants(B, Hq, Hkv, D, P, max_pages, cap, ns_req):
+def test_split_grid_plan_invariants(B, Hq, Hkv, D, P, max_pages, cap, ns_req):
     p = plan(B, Hq, Hkv, D, P, max_pages, cap, ns_req, num_cus=256)
+    assert p["schedule"] == "split_grid"
     ns, tps, ws = p["splits"], p["tokens_per_split"], p["workspace_bytes"]
     table_tokens = max_pages * P
     eff_cap = cap if 0 < cap < table_tokens else table_tokens
@@ -167,22 +171,49 @@ def test_plan_invariants(B, Hq, Hkv, D, P, max_pages, cap, ns_req):
     assert tps % P == 0 and tps >= P
     assert ns * tps >= eff_cap                      # every capacity token is covered
     assert (ns - 1) * tps < eff_cap                 # and no split is empty at capacity
+    assert p["workgroups"] == B * Hkv * ns
     if ns_req > 0:
         assert ns <= ns_req
     if ns == 1:
         assert ws == 256
     else:
         rows = B * Hq * ns
-        assert ws == 256 + math.ceil(rows * 4 / 256) * 256 + rows * D * 4
+        assert ws == PARTIAL_BASE + math.ceil(rows * 4 / 256) * 256 + rows * D * 4
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,ns_req,groups", [
+    (64, 32, 8, 128, 0, 256),      # automatic: one 4-wave workgroup per CU at D=128
+    (128, 32, 4, 64, 0, 512),      # two 2-wave workgroups per CU at D=64
+    (64, 16, 2, 256, 0, 256),      # one per CU at D=256
+    (4, 32, 8, 128, -7, 7),        # forced workgroup count
+    (512, 28, 4, 128, 0, 256),
+    (3, 32, 8, 128, -9000, 4095),  # clamped to the 8^4 merge tree
+])
+def test_balanced_plan(B, Hq, Hkv, D, ns_req, groups):
+    p = plan(B, Hq, Hkv, D, 16, 64, 0, ns_req, num_cus=256)
+    assert p["schedule"] == "balanced"
+    assert p["workgroups"] == groups and p["splits"] == 0
+    slots = groups + B * Hkv
+    G = Hq // Hkv
+    o_off = PARTIAL_BASE + math.ceil(slots * G * 4 / 256) * 256
+    assert p["workspace_bytes"] == o_off + slots * G * D * 4
 
 
 def test_policy_on_the_north_star_configs():
-    """Split counts the automatic policy picks for a 256-CU MI355X (measured optima: see the
-    split sweep in the design notes)."""
-    expect = {"llama3_8b": 1, "long_b1_128k": 64, "long_b4_32k": 16, "sweep_d64": 2,
-              "sweep_d256": 8}
-    for name, ns in expect.items():
-        s = W.NORTH_STAR[name]
-        got = plan(s.batch, s.num_heads, s.num_kv_heads, s.head_dim, s.page_size, s.max_pages,
-                   num_cus=256)["splits"]
-        assert got == ns, f"{name}: {got} != {ns}"
+    """The automatic plan on a 256-CU MI355X (from interleaved A/B sweeps): batches of at
+    least 64 (sequence, KV head) units take the balanced single launch; fewer, long units take
+    the split grid with about one workgroup per CU."""
+    expect = {
+        "tiny": ("split_grid", 4), "llama3_8b": ("balanced", 256),
+        "long_b1_32k": ("split_grid", 32), "long_b1_128k": ("split_grid", 32),
+        "long_b4_32k": ("split_grid", 8), "long_b4_128k": ("split_grid", 8),
+        "ragged": ("balanced", 256), "sweep_b32_16k": ("balanced", 256),
+        "sweep_b128_16k": ("balanced", 256), "sweep_d64": ("balanced", 512),
+        "sweep_d256": ("balanced", 256),
+    }
+    for name, s in W.NORTH_STAR.items():
+        p = plan(s.batch, s.num_heads, s.num_kv_heads, s.head_dim, s.page_size, s.max_pages,
+                 num_cus=256)
+        sched, n = expect[name]
+        assert p["schedule"] == sched, name
+        assert (p["workgroups"] if sched == "balanced" else p["splits"]) == n, name
