@@ -745,50 +745,71 @@ void mx_paged_decode_balanced(
                      f32x4{0.f, 0.f, 0.f, 0.f});
   }
 
-  // Pass 1: total positions.
+  // Sequence weights (positions per sequence).  The batch is at most 512 sequences, so every
+  // thread reads its few seq_lens once and keeps their weights in registers for both the total
+  // and the scan that locates this workgroup's first position.
+  constexpr int kScanPerThread = (512 + 64 * NW - 1) / (64 * NW);
   auto weight = [&](int b, bool report) -> int {
     const int seq = clamped_len(seq_lens, b, sh, status, report);
     return seq > 0 ? Hkv * ((seq + kChunk - 1) / kChunk + alpha) : 0;
   };
-  int total = 0;
-  for (int base = 0; base < B; base += 64 * NW) {
-    const int b = base + tid;
-    total += block_sum<NW>(b < B ? weight(b, wg == 0) : 0, s_int);
+  int wts[kScanPerThread];
+  int mine = 0;
+#pragma unroll
+  for (int i = 0; i < kScanPerThread; ++i) {
+    const int b = i * 64 * NW + tid;
+    wts[i] = b < B ? weight(b, wg == 0) : 0;
+    mine += wts[i];
   }
+  // Total positions of the batch.
+  int incl = mine;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off);
+    if (lane >= off) incl += y;
+  }
+  if (tid == 0) s_int[NW] = -1;
+  if (lane == 63) s_int[wv] = incl;
+  __syncthreads();
+  int total = 0;
+#pragma unroll
+  for (int w2 = 0; w2 < NW; ++w2) total += s_int[w2];
   if (total == 0) return;
   const int qsz = (total + sh.num_groups - 1) / sh.num_groups;
   const int x_begin = wg * qsz;
   if (x_begin >= total) return;
   const int x_end = min(x_begin + qsz, total);
-
-  // Pass 2: the sequence holding position x_begin and the position where it starts.
-  if (tid == 0) s_int[NW] = -1;
-  int carry = 0;
-  for (int base = 0; base < B; base += 64 * NW) {
-    const int b = base + tid;
-    const int w = b < B ? weight(b, false) : 0;
-    int incl = w;
+  // Positions are laid out sequence by sequence: thread tid's i-th sequence b = i*64*NW + tid
+  // starts after all sequences of smaller index, i.e. after blocks < i of every thread plus
+  // the block-i sequences of lower threads.  Blocks are scanned one at a time.
+  {
+    int carry = 0;
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int y = __shfl_up(incl, off);
-      if (lane >= off) incl += y;
+    for (int i = 0; i < kScanPerThread; ++i) {
+      int incl_i = wts[i];
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(incl_i, off);
+        if (lane >= off) incl_i += y;
+      }
+      __syncthreads();
+      if (lane == 63) s_int[wv] = incl_i;
+      __syncthreads();
+      int blk_before = 0, blk_total = 0;
+#pragma unroll
+      for (int w2 = 0; w2 < NW; ++w2) {
+        blk_before += (w2 < wv) ? s_int[w2] : 0;
+        blk_total += s_int[w2];
+      }
+      const int start = carry + blk_before + incl_i - wts[i];
+      if (wts[i] > 0 && start <= x_begin && x_begin < start + wts[i]) {
+        s_int[NW] = i * 64 * NW + tid;
+        s_int[NW + 1] = start;
+      }
+      carry += blk_total;
+      if (carry > x_begin) break;  // uniform: carry is the same in every thread
     }
     __syncthreads();
-    if (lane == 63) s_int[wv] = incl;
-    __syncthreads();
-    int before = carry;
-    for (int w2 = 0; w2 < wv; ++w2) before += s_int[w2];
-    const int start = before + incl - w;
-    if (w > 0 && start <= x_begin && x_begin < start + w) {
-      s_int[NW] = b;
-      s_int[NW + 1] = start;
-    }
-    int blk = 0;
-#pragma unroll
-    for (int w2 = 0; w2 < NW; ++w2) blk += s_int[w2];
-    carry += blk;
-    __syncthreads();
-    if (carry > x_begin) break;  // uniform: every thread holds the same carry
   }
   int b = __builtin_amdgcn_readfirstlane(s_int[NW]);
   int seq_start = __builtin_amdgcn_readfirstlane(s_int[NW + 1]);
@@ -872,23 +893,25 @@ void mx_paged_decode_balanced(
             const int hh = e / (D / 4);
             const int d = 4 * (e - hh * (D / 4));
             float mx = -INFINITY;
+            // All log-sum-exps and partial vectors of the group are loaded in one round.
             float lses[kMergeFanIn];
+            f32x4 vals[kMergeFanIn];
 #pragma unroll
             for (int t = 0; t < kMergeFanIn; ++t) {
-              lses[t] = t < gsize ? load_partial1(part_lse + (int64_t)(gslot + t * stride) * G + hh)
-                                  : -INFINITY;
-              mx = fmaxf(mx, lses[t]);
+              const int64_t sl = gslot + t * stride;
+              lses[t] = t < gsize ? load_partial1(part_lse + sl * G + hh) : -INFINITY;
+              vals[t] = t < gsize ? load_partial4(part_o + (sl * G + hh) * D + d)
+                                  : f32x4{0.f, 0.f, 0.f, 0.f};
             }
+#pragma unroll
+            for (int t = 0; t < kMergeFanIn; ++t) mx = fmaxf(mx, lses[t]);
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
             float wsum = 0.f;
 #pragma unroll
             for (int t = 0; t < kMergeFanIn; ++t) {
-              if (t < gsize) {
-                const int64_t sl = gslot + t * stride;
-                const float w = __builtin_amdgcn_exp2f(lses[t] - mx);
-                wsum += w;
-                acc += w * load_partial4(part_o + (sl * G + hh) * D + d);
-              }
+              const float w = __builtin_amdgcn_exp2f(lses[t] - mx);  // 0 for t >= gsize
+              wsum += w;
+              acc += w * vals[t];
             }
             acc *= 1.0f / wsum;
             if (nnext == 1) {

@@ -363,3 +363,17 @@ def test_library_workspace_survives_schedule_and_shape_changes():
         _check(inp, out, _sample(inp.spec.batch, 8), label=f"{name} ns={ns}")
         assert read_device_status() == 0
         del inp
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D", [(500, 16, 2, 128), (400, 16, 4, 64), (300, 8, 1, 256)])
+def test_balanced_multi_block_length_scan(B, Hq, Hkv, D):
+    """Batches whose seq_lens scan spans several blocks of the workgroup's threads."""
+    g = torch.Generator().manual_seed(B)
+    lens = torch.randint(0, 700, (B,), generator=g).tolist()
+    lens[0], lens[-1] = 1, 700
+    spec = W.custom_spec(f"scan{B}", lens, Hq, Hkv, D, 16)
+    inp = W.make_inputs(spec, seed=B, device=DEV)
+    for ns in (0, -3, -257):
+        out = _decode(inp, num_splits=ns)
+        _check(inp, out, _sample(B, 24, seed=B), label=f"B={B} D={D} ns={ns}")
+        assert read_device_status() == 0
