@@ -2,14 +2,19 @@
  * mx_paged_decode.h -- C ABI of the MI355X (gfx950) paged GQA decode attention library
  * (libmxattn.so).
  *
- * Operator (reference task.md:138-148): for every sequence b and query head h,
+ * Operator (reference task.md:138-148): for every sequence b, query token i < seqlen_q and
+ * query head h,
  *   kv      = h / (num_heads / num_kv_heads)
- *   tokens  = the first seq_lens[b] tokens of sequence b; token t lives in physical page
- *             block_table[b, t / page_size] at in-page offset t % page_size
- *   out[b,h,:] = softmax(q[b,h,:] . K[tokens,kv,:]^T * scale) . V[tokens,kv,:]
+ *   keys    = the first L = seq_lens[b] tokens of sequence b; token t lives in physical page
+ *             block_table[b, t / page_size] at in-page offset t % page_size.  With causal = 1
+ *             query token i sees only keys t < L - seqlen_q + i + 1 (the causal mask aligned to
+ *             the end of the cache, as flash_attn_with_kvcache does for the reference's
+ *             seqlen_q / causal arguments, task.md:47, 53); a query row that sees no key is
+ *             written as zeros, as is every row of an empty sequence (L <= 0).
+ *   out[b,i,h,:] = softmax(q[b,i,h,:] . K[keys,kv,:]^T * scale) . V[keys,kv,:]
  *
  * Layouts (all contiguous, row-major):
- *   q, out       [batch, num_heads, head_dim]            bf16  (== [batch, 1, num_heads, head_dim])
+ *   q, out       [batch, seqlen_q, num_heads, head_dim]  bf16  (seqlen_q == 1 is the decode step)
  *   k/v cache    [num_pages, page_size, num_kv_heads, head_dim]  bf16
  *   seq_lens     [batch]                                  int32
  *   block_table  [batch, max_pages_per_seq]               int32
@@ -17,7 +22,10 @@
  * padding entries after them are never touched (reference task.md:8-10, 61, 92).
  *
  * Supported shapes: head_dim in {64, 128, 256}; page_size in {16, 32, 64, 128, 256};
- * num_heads % num_kv_heads == 0 and num_heads / num_kv_heads <= 16; seqlen_q == 1; causal == 0.
+ * num_heads % num_kv_heads == 0 and num_heads / num_kv_heads <= 16; seqlen_q >= 1 with
+ * batch * seqlen_q <= 65535; causal 0 or 1.  The seqlen_q * (num_heads / num_kv_heads) query
+ * rows of one KV head are processed 16 at a time: every further 16 rows stream that head's
+ * K/V once more.
  *
  * Every call is asynchronous on the given stream (NULL = the legacy default stream) and never
  * synchronises.  Calls that share one workspace (including the library's internal one) must
@@ -47,7 +55,8 @@ extern "C" {
 #define MX_DEVICE_SEQ_TOO_LONG 2u   /* seq_lens[b] exceeded the capacity the call was planned for */
 
 /* Schedules reported by mx_paged_gqa_decode_plan. */
-#define MX_SCHEDULE_SPLIT_GRID 0   /* grid (Hkv, batch, splits) + combine kernel when splits > 1  */
+#define MX_SCHEDULE_SPLIT_GRID 0   /* grid (Hkv * row tiles, batch, splits) + combine kernel
+                                      when splits > 1                                             */
 #define MX_SCHEDULE_BALANCED 1     /* one launch of a fixed number of workgroups that divide the
                                       batch's K/V chunks evenly from seq_lens on the device and
                                       merge split sequences themselves                            */
@@ -66,7 +75,9 @@ extern "C" {
  *   - block_table row width = num_blocks / batch_size (submission_clean.cu:449, task.md:61);
  *   - seqlen_k is the capacity used for split planning (task.md:7, 131);
  *   - launches on the legacy default stream, no synchronisation (task.md:67);
- *   - uses a library-owned, grow-only workspace per device (submission_clean.cu:478-491).
+ *   - uses a library-owned, grow-only workspace per device (submission_clean.cu:478-491);
+ *   - seqlen_q >= 1 and causal (0 or 1) are honoured with the operator semantics above (the
+ *     reference fixes them at 1 and 0, task.md:64, 66, and its kernel ignores them).
  * Returns nothing, as the reference does; on invalid arguments nothing is launched, a message
  * is printed to stderr and the status is kept for mx_last_status() / mx_last_error().
  */
@@ -79,6 +90,7 @@ void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_pa
 /*
  * Extended entry point (replaces the same run_kernel, submission_clean.cu:432-504, with an
  * explicit scale, table width, pool size, split override, workspace and stream, and a status).
+ *   seqlen_q           query tokens per sequence (1 = decode).
  *   num_pages          pool size; page ids outside [0, num_pages) are flagged and read as page 0.
  *                      0 = unknown (only negative ids are flagged).
  *   max_pages_per_seq  block_table row width.
@@ -86,9 +98,11 @@ void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_pa
  *                      seq_lens[b] beyond the planned capacity (max_seq_len rounded up to whole
  *                      splits, at most max_pages_per_seq*page_size) are clamped and flagged
  *                      (MX_DEVICE_SEQ_TOO_LONG).
+ *   causal             0, or 1 for the end-aligned causal mask of multi-token queries.
  *   num_splits         0 = automatic: the balanced schedule when batch <= 512 and
- *                      64 <= batch * num_kv_heads <= 8192, else the split grid with a
- *                      CU-count-driven split count;
+ *                      64 <= units <= 8192 (units = batch * num_kv_heads *
+ *                      ceil(seqlen_q * num_heads / num_kv_heads / 16)), else the split grid
+ *                      with a CU-count-driven split count;
  *                      > 0 = split grid with that many splits per sequence (clamped to the
  *                      number of pages of max_seq_len);
  *                      < 0 = balanced schedule with exactly -num_splits workgroups.
@@ -102,10 +116,11 @@ void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_pa
  */
 int mx_paged_gqa_decode(const void* q, const void* k_cache, const void* v_cache, void* out,
                         const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
-                        int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
-                        int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
-                        int64_t max_seq_len, float scale, int64_t num_splits, void* workspace,
-                        int64_t workspace_bytes, int32_t phase, void* stream);
+                        int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads,
+                        int64_t head_dim, int64_t page_size, int64_t num_pages,
+                        int64_t max_pages_per_seq, int64_t max_seq_len, int32_t causal,
+                        float scale, int64_t num_splits, void* workspace, int64_t workspace_bytes,
+                        int32_t phase, void* stream);
 
 /*
  * Host-only planning (no HIP call when num_cus > 0): validates the shape and reports the
@@ -115,17 +130,17 @@ int mx_paged_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
  * (submission_clean.cu:375-430) and its page-rounding of splits (submission_clean.cu:456-461).
  * num_cus <= 0 queries the current device.  Any of the out pointers may be NULL.
  */
-int mx_paged_gqa_decode_plan(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
-                             int64_t head_dim, int64_t page_size, int64_t max_pages_per_seq,
-                             int64_t max_seq_len, int64_t num_splits, int64_t num_cus,
-                             int64_t* schedule_out, int64_t* splits_out,
+int mx_paged_gqa_decode_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads,
+                             int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                             int64_t max_pages_per_seq, int64_t max_seq_len, int64_t num_splits,
+                             int64_t num_cus, int64_t* schedule_out, int64_t* splits_out,
                              int64_t* tokens_per_split_out, int64_t* workgroups_out,
                              int64_t* workspace_bytes_out);
 
 /* Workspace bytes a call needs (replaces the grow-only sizing of submission_clean.cu:463,
  * 478-491); negative MX_STATUS_* on invalid arguments.  Queries the current device's CU count
  * when num_splits == 0. */
-int64_t mx_paged_gqa_decode_workspace_size(int64_t batch, int64_t num_heads,
+int64_t mx_paged_gqa_decode_workspace_size(int64_t batch, int64_t seqlen_q, int64_t num_heads,
                                            int64_t num_kv_heads, int64_t head_dim,
                                            int64_t page_size, int64_t max_pages_per_seq,
                                            int64_t max_seq_len, int64_t num_splits);

@@ -1,30 +1,30 @@
-// Paged GQA decode attention for MI355X (gfx950): split-KV main kernel, log-sum-exp combine
-// kernel, split policy, argument validation and the C ABI declared in include/mx_paged_decode.h.
+// Paged GQA decode attention for MI355X (gfx950): split-KV and length-balanced main kernels,
+// log-sum-exp combine kernel, schedule policy, argument validation and the C ABI declared in
+// include/mx_paged_decode.h.
 //
-// Operator: reference task.md:138-148 (one query token per sequence, paged bf16 K/V cache,
-// query head h reads KV head h / group).  The reference's kernel pair is
-// submission_clean.cu:66-300 (main) and :307-360 (combine); its launcher is :432-504.  The
-// softmax here is the running-max form of optimized_c500_flash_attn.cu:310-461 (page max,
-// rescale) and its combine the LSE merge of optimized_c500_flash_attn.cu:666-728.
+// Operator: reference task.md:138-148 (paged bf16 K/V cache, query head h reads KV head
+// h / group), extended to seqlen_q query tokens per sequence with the optional end-aligned
+// causal mask (task.md:47, 53).  The reference's kernel pair is submission_clean.cu:66-300
+// (main) and :307-360 (combine); its launcher is :432-504.  The softmax is the running-max form
+// of optimized_c500_flash_attn.cu:310-461 and the merge the LSE combine of :666-728.
 //
 // Design (gfx950, wave64):
-//  * One 64-lane wave per (KV head, split, sequence); grid (Hkv, splits, batch) so the Hkv
-//    waves that stream the same physical pages are dispatched back to back.
-//  * No LDS.  A 16-token chunk of K is loaded straight into the A operand of
-//    v_mfma_f32_16x16x32_bf16 (lane = token r16, 8 consecutive dims per k-group g4) and the
-//    product is S^T = K . Q^T with the query group as the N dimension.  The 16x16 fp32 result
-//    leaves lane (head r16, g4) holding the scores of tokens 4*g4 .. 4*g4+3, which is exactly the
-//    B-operand layout of v_mfma_f32_16x16x16_bf16 for O^T = V^T . P^T, so P never moves.
-//  * V is loaded as whole 2*D-byte token rows (lane (r16, g4) reads rows 4*g4+r, dims
-//    (D/16)*r16 ..) and v_perm_b32 regroups the bf16 halves into V^T operands; PV tile i holds
-//    dims d = (D/16)*m + i, so lane (h, g4) ends with the contiguous dims [D/4*g4, D/4*(g4+1)).
-//  * K/V chunks are double-buffered in registers; the loop body issues no conditional loads so
-//    the compiler's vmcnt waits stay partial.
-//  * Online softmax in fp32, log2 domain, with a lazy rescale: the running max only moves when
-//    a chunk max exceeds it by more than 8, so p <= 2^8 and the O/l rescale is rare.  The final
-//    normalisation uses the same max for numerator and denominator, so the result is exact.
-//  * Sequences that fit one split write bf16 output directly; longer ones write normalised fp32
-//    partials plus a log2-sum-exp per (head, split), merged by the combine kernel.
+//  * Query rows (token, head of the group) of one KV head are the N dimension of the MFMAs:
+//    QK is S^T = K . Q^T with v_mfma_f32_16x16x32_bf16 (16 tokens x 16 rows), whose fp32 result
+//    leaves lane (row r16, k-group g4) holding the scores of tokens 4*g4 .. 4*g4+3 -- exactly
+//    the B operand of v_mfma_f32_16x16x16_bf16 for O^T = V^T . P^T, so P never moves.
+//  * K and V are loaded as whole 2*D-byte token rows (nontemporal); K goes through a
+//    wave-private XOR-swizzled LDS tile into the MFMA A layout, V is regrouped by v_perm_b32.
+//  * Each wave streams 16-token chunks through a register ring with unconditional refills (so
+//    vmcnt waits stay partial); NW waves of a workgroup interleave the chunks of one piece and
+//    merge their (m, l, O) states through LDS.
+//  * Online softmax in fp32, log2 domain, lazy rescale (the running max moves only when a
+//    chunk max exceeds it by more than 8); the final O / l uses one max for both, so it is
+//    exact.  Masked chunks (sequence tail, causal limits) use selects, never arithmetic on
+//    unused page slots.
+//  * Two schedules: the split grid (Hkv * row tiles, batch, splits) plus a combine kernel, and
+//    a single length-balanced launch that cuts the batch's chunk line into equal shares on the
+//    device and merges cut units through a fan-in-8 tree of arrival counters.
 
 #include <hip/hip_runtime.h>
 
@@ -275,20 +275,35 @@ __device__ __forceinline__ void k_operands(bf16x8 (&kop)[D / 32], const Chunk<D>
   }
 }
 
+// Initial running max: finite, so exp2(score - m) is 0 for a masked (-inf) score even before a
+// row has seen any visible key; a row that never sees one keeps l == 0 and is written as zeros.
+constexpr float kNoScore = -1.0e30f;
+
 template <int D>
 struct SoftmaxState {
-  f32x4 o[D / 16];  // o[i][j] = O[head r16][(D/16)*(4*g4 + j) + i]
-  float m;          // running max (log2 units), identical on the 4 lanes of a head
+  f32x4 o[D / 16];  // o[i][j] = O[row r16][(D/16)*(4*g4 + j) + i]
+  float m;          // running max (log2 units), identical on the 4 lanes of a row
   float l;          // this lane's share of the running denominator
 };
 
+template <int D>
+__device__ __forceinline__ void reset_state(SoftmaxState<D>& st) {
+#pragma unroll
+  for (int i = 0; i < D / 16; ++i) st.o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  st.m = kNoScore;
+  st.l = 0.f;
+}
+
 // One chunk of the online softmax.  kMasked: only the first `nvalid` tokens of the chunk are
-// real; the scores of the others become -inf and their V rows are replaced by zeros (so NaN or
-// Inf in unused page slots cannot reach the accumulators).
+// real (their V rows are kept, the others are replaced by zeros, so NaN or Inf in unused page
+// slots cannot reach the accumulators), and this lane's query row sees only the first
+// `row_valid` (<= nvalid) tokens: the causal limit of multi-token queries.  Scores of tokens a
+// row does not see become -inf.
 template <int D, bool kMasked>
 __device__ __forceinline__ void process_chunk(SoftmaxState<D>& st, const Chunk<D>& c,
                                               const bf16x8 (&qop)[D / 32], float scale_log2,
-                                              int g4, int nvalid, char* klds, int lane) {
+                                              int g4, int nvalid, int row_valid, char* klds,
+                                              int lane) {
   // S^T[token][head] = K . Q^T  (16 tokens x 16 head slots, contraction over D)
   bf16x8 kop[D / 32];
   k_operands<D>(kop, c, klds, lane);
@@ -301,7 +316,7 @@ __device__ __forceinline__ void process_chunk(SoftmaxState<D>& st, const Chunk<D
   for (int j = 0; j < 4; ++j) {
     x[j] = s[j] * scale_log2;
     if constexpr (kMasked) {
-      if (4 * g4 + j >= nvalid) x[j] = -INFINITY;
+      if (4 * g4 + j >= row_valid) x[j] = -INFINITY;
     }
   }
   float cm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
@@ -344,12 +359,22 @@ __device__ __forceinline__ void process_chunk(SoftmaxState<D>& st, const Chunk<D
 // Shared pieces of the main kernels
 // ------------------------------------------------------------------------------------------
 
+// Query rows.  The seqlen_q query tokens of a sequence times the G query heads of one KV head
+// form rows r = t * G + h (token t, head h); rows are processed in tiles of 16 (the N dimension
+// of the QK MFMA), so a unit of work is one (sequence, KV head, row tile) and kvr = kv *
+// row_tiles + tile indexes the second and third.
 struct MainShape {
   int64_t page_stride;   // elements between physical pages: page_size * Hkv * D
   int token_stride;      // elements between tokens of a page: Hkv * D
   int num_heads;
   int num_kv_heads;
   int group;
+  uint32_t group_magic;  // floor(2^32 / group) + 1 (0 when group == 1): r / group by mul-high
+  int seqlen_q;          // query tokens per sequence
+  int causal;            // row t sees keys [0, L - seqlen_q + t + 1) (bottom-right aligned)
+  int rows;              // seqlen_q * group
+  int row_tiles;         // ceil(rows / 16)
+  int tile_rows;         // min(rows, 16): rows per tile slot of the partial buffers
   int batch;
   int max_pages;         // block_table row width
   int num_pages;         // pool size, 0 = unknown
@@ -376,32 +401,56 @@ __device__ __forceinline__ int clamped_len(const int32_t* seq_lens, int b, const
   return seq;
 }
 
-// Query operand of (b, kv): lane (h, g4) holds Q[kv*G + h][32*i + 8*g4 .. +7] for MFMA i.
+// Rows of q / out.  Row r = t*G + h of KV head kv of sequence b is q row
+// (b*seqlen_q + t)*num_heads + kv*G + h = row_base(b, kv) + row_offset(r): a wave-uniform base
+// plus a per-lane offset that is r itself for a single query token.
+__device__ __forceinline__ int64_t row_base(int b, int kv, const MainShape& sh) {
+  return (int64_t)b * sh.seqlen_q * sh.num_heads + kv * sh.group;
+}
+// Query token of row r: r / group, exact for 0 <= r < 2^32 / group.
+__device__ __forceinline__ int row_token(int r, const MainShape& sh) {
+  return sh.group_magic ? (int)__umulhi((uint32_t)r, sh.group_magic) : r;
+}
+__device__ __forceinline__ int row_offset(int r, const MainShape& sh) {
+  return r + row_token(r, sh) * (sh.num_heads - sh.group);
+}
+
+// Keys row r of a sequence of length seq sees: [0, limit).
+__device__ __forceinline__ int row_key_limit(int r, int seq, const MainShape& sh) {
+  if (!sh.causal) return seq;
+  return seq - sh.seqlen_q + row_token(min(r, sh.rows - 1), sh) + 1;
+}
+
+// Query operand of row tile `tile` of (b, kv): lane (r16, g4) holds row tile*16 + r16,
+// dims 32*i + 8*g4 .. +7, for MFMA i (zeros past the last row).
 template <int D>
 __device__ __forceinline__ void load_q(bf16x8 (&qop)[D / 32], const uint16_t* q, int b, int kv,
-                                       const MainShape& sh, int lane) {
-  const int h = lane & 15;
+                                       int tile, const MainShape& sh, int lane) {
   const int g4 = lane >> 4;
-  const uint16_t* qp = q + ((int64_t)b * sh.num_heads + kv * sh.group + h) * D + 8 * g4;
+  const int r = tile * 16 + (lane & 15);
+  const bool live = r < sh.rows;
+  const uint16_t* qp = q + (row_base(b, kv, sh) + (live ? row_offset(r, sh) : 0)) * D + 8 * g4;
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) {
     u32x4 x = {0, 0, 0, 0};
-    if (h < sh.group) x = *reinterpret_cast<const u32x4*>(qp + 32 * i);
+    if (live) x = *reinterpret_cast<const u32x4*>(qp + 32 * i);
     qop[i] = __builtin_bit_cast(bf16x8, x);
   }
 }
 
-// Streams chunks c_lo + wv + k*NW (k >= 0, < c_hi) of sequence b, KV head kv through this
-// wave's register ring, accumulating into `st`.  Chunk c_last is the sequence's last chunk and
-// holds `last_valid` tokens.
-template <int D, int NBUF, int NW>
+// Streams chunks c_lo + wv + k*NW (k >= 0, < c_hi) of one (sequence, KV head) through this
+// wave's register ring, accumulating into `st`.  The sequence holds `seq` tokens; chunks from
+// c_mask on (at least the last one) are processed with masks: tokens past the sequence end,
+// and with kCausal, for this lane's query row, the keys at or past row_lim.  Without kCausal
+// c_mask is the last chunk and row_lim is ignored.
+template <int D, int NBUF, int NW, bool kCausal>
 __device__ __forceinline__ void stream_chunks(SoftmaxState<D>& st, const bf16x8 (&qop)[D / 32],
                                               const uint16_t* __restrict__ kc,
                                               const uint16_t* __restrict__ vc,
                                               const int32_t* __restrict__ bt_row, int kv,
-                                              int c_lo, int c_hi, int c_last, int last_valid,
-                                              int wv, char* klds, const MainShape& sh,
-                                              bool& bad_page) {
+                                              int c_lo, int c_hi, int seq, int c_mask,
+                                              int row_lim, int wv, char* klds,
+                                              const MainShape& sh, bool& bad_page) {
   constexpr int VW = D / 16;
   const int lane = threadIdx.x & 63;
   const int r16 = lane & 15;
@@ -425,28 +474,50 @@ __device__ __forceinline__ void stream_chunks(SoftmaxState<D>& st, const bf16x8 
   };
   const int n = (c_hi - c_lo > wv) ? (c_hi - c_lo - wv + NW - 1) / NW : 0;
   auto gc = [&](int k) { return c_lo + wv + k * NW; };
-  auto nvalid_of = [&](int k) { return gc(k) == c_last ? last_valid : kChunk; };
+  // Masked processing of this wave's k-th chunk: tokens of the chunk inside the sequence, and
+  // those this lane's row sees.
+  auto masked = [&](Chunk<D>& cb, int k) {
+    const int t0 = gc(k) * kChunk;
+    const int nvalid = min(kChunk, seq - t0);
+    const int row_valid = kCausal ? min(nvalid, row_lim - t0) : nvalid;
+    process_chunk<D, true>(st, cb, qop, sl2, g4, nvalid, row_valid, klds, lane);
+  };
 
   Chunk<D> buf[NBUF];
   auto load = [&](Chunk<D>& dst, int64_t base) { load_chunk<D>(dst, kc + base, vc + base, lo); };
 
-  // Register ring of NBUF chunks.  The steady-state loop processes NBUF full chunks and
-  // refills their buffers with the next NBUF, with no conditional loads (so the compiler's
-  // vmcnt waits stay partial); the page lookups of the refills are issued before the math.
+  // Register ring of NBUF chunks.  The steady-state loops process NBUF chunks and refill their
+  // buffers with the next NBUF, with no conditional loads (so the compiler's vmcnt waits stay
+  // partial); the page lookups of the refills are issued before the math.  Chunks before
+  // c_mask need no mask; the second loop only runs when masking starts early (causal queries
+  // with many tokens).
   if (n >= NBUF) {
 #pragma unroll
     for (int i = 0; i < NBUF; ++i) load(buf[i], chunk_base(gc(i)));
     int k = 0;
-    while (k + 2 * NBUF <= n) {
+    while (k + 2 * NBUF <= n && (!kCausal || gc(k + NBUF - 1) < c_mask)) {
       int64_t nb[NBUF];
 #pragma unroll
       for (int i = 0; i < NBUF; ++i) nb[i] = chunk_base(gc(k + NBUF + i));
 #pragma unroll
       for (int i = 0; i < NBUF; ++i) {
-        process_chunk<D, false>(st, buf[i], qop, sl2, g4, kChunk, klds, lane);
+        process_chunk<D, false>(st, buf[i], qop, sl2, g4, kChunk, kChunk, klds, lane);
         load(buf[i], nb[i]);
       }
       k += NBUF;
+    }
+    if constexpr (kCausal) {
+      while (k + 2 * NBUF <= n) {
+        int64_t nb[NBUF];
+#pragma unroll
+        for (int i = 0; i < NBUF; ++i) nb[i] = chunk_base(gc(k + NBUF + i));
+#pragma unroll
+        for (int i = 0; i < NBUF; ++i) {
+          masked(buf[i], k + i);
+          load(buf[i], nb[i]);
+        }
+        k += NBUF;
+      }
     }
     // k + NBUF <= n < k + 2*NBUF: buffers hold chunks k .. k+NBUF-1, `extra` more remain.
     const int extra = n - k - NBUF;
@@ -454,23 +525,22 @@ __device__ __forceinline__ void stream_chunks(SoftmaxState<D>& st, const bf16x8 
     for (int i = 0; i < NBUF; ++i) {
       if (i < extra) {
         const int64_t nbase = chunk_base(gc(k + NBUF + i));
-        process_chunk<D, true>(st, buf[i], qop, sl2, g4, nvalid_of(k + i), klds, lane);
+        masked(buf[i], k + i);
         load(buf[i], nbase);
       } else {
-        process_chunk<D, true>(st, buf[i], qop, sl2, g4, nvalid_of(k + i), klds, lane);
+        masked(buf[i], k + i);
       }
     }
 #pragma unroll
     for (int i = 0; i < NBUF; ++i)
-      if (i < extra)
-        process_chunk<D, true>(st, buf[i], qop, sl2, g4, nvalid_of(k + NBUF + i), klds, lane);
+      if (i < extra) masked(buf[i], k + NBUF + i);
   } else {
 #pragma unroll
     for (int i = 0; i < NBUF; ++i)
       if (i < n) load(buf[i], chunk_base(gc(i)));
 #pragma unroll
     for (int i = 0; i < NBUF; ++i)
-      if (i < n) process_chunk<D, true>(st, buf[i], qop, sl2, g4, nvalid_of(i), klds, lane);
+      if (i < n) masked(buf[i], i);
   }
 }
 
@@ -514,7 +584,8 @@ __device__ __forceinline__ void publish_wave_state(char* lds, const SoftmaxState
   __syncthreads();
 }
 
-// Merged (normalised) dims d..d+3 of head slot hh and its log2-sum-exp.
+// Merged (normalised) dims d..d+3 of row slot hh and its log2-sum-exp; a row that saw no key
+// (l == 0: causal rows before their first key) is zeros with log2-sum-exp -inf.
 template <int D, int NW>
 __device__ __forceinline__ f32x4 merged_head(const char* lds, int hh, int d, float& lse) {
   using L = GroupLds<D, NW>;
@@ -532,8 +603,9 @@ __device__ __forceinline__ f32x4 merged_head(const char* lds, int hh, int d, flo
     acc += a * *reinterpret_cast<const f32x4*>(L::o(const_cast<char*>(lds)) +
                                               (w * 16 + hh) * L::kRow + d);
   }
-  lse = mx + log2f(lsum);
-  return acc * (1.0f / lsum);
+  const bool seen = lsum > 0.f;
+  lse = seen ? mx + log2f(lsum) : -INFINITY;
+  return acc * (seen ? 1.0f / lsum : 0.f);
 }
 
 __device__ __forceinline__ void store_bf16x4(uint16_t* p, f32x4 v) {
@@ -545,16 +617,17 @@ __device__ __forceinline__ void store_bf16x4(uint16_t* p, f32x4 v) {
 // Split-grid kernel
 // ------------------------------------------------------------------------------------------
 
-// Grid (Hkv, batch, splits), NW waves per workgroup.  Consecutive workgroup ids, which the
-// dispatcher deals round-robin to the 8 XCDs, walk the KV heads of one sequence first, then
-// the sequences, then the splits.  Every XCD therefore gets an even share of the first split
-// of every sequence (where ragged batches keep most of their work), and the Hkv workgroups
-// that read the same physical pages start together.
+// Grid (Hkv * row_tiles, batch, splits), NW waves per workgroup.  Consecutive workgroup ids,
+// which the dispatcher deals round-robin to the 8 XCDs, walk the KV heads (and row tiles) of
+// one sequence first, then the sequences, then the splits.  Every XCD therefore gets an even
+// share of the first split of every sequence (where ragged batches keep most of their work),
+// and the workgroups that read the same physical pages start together.
 //
-// The NW waves of a workgroup share one (KV head, sequence, split): wave wv streams chunks
-// c0+wv, c0+wv+NW, ... through its own register ring (so NW times more K/V bytes are in flight
-// per split, with no global partials), and the waves merge their (m, l, O) states through LDS.
-template <int D, int NBUF, int NW>
+// The NW waves of a workgroup share one (KV head, row tile, sequence, split): wave wv streams
+// chunks c0+wv, c0+wv+NW, ... through its own register ring (so NW times more K/V bytes are in
+// flight per split, with no global partials), and the waves merge their (m, l, O) states
+// through LDS.
+template <int D, int NBUF, int NW, bool kCausal>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     D == 64 ? MX_WAVES_PER_EU_D64 : (D == 128 ? MX_WAVES_PER_EU_D128 : MX_WAVES_PER_EU_D256))))
 void mx_paged_decode_splitkv(
@@ -570,45 +643,48 @@ void mx_paged_decode_splitkv(
   // Wave index, made provably wave-uniform so the chunk indices derived from it stay in
   // SGPRs and the page lookups remain scalar loads (off the vector-memory counter).
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kv = blockIdx.x;
+  const int kv = blockIdx.x / sh.row_tiles;
+  const int tile = blockIdx.x - kv * sh.row_tiles;
   const int b = blockIdx.y;
   const int split = blockIdx.z;
-  const int G = sh.group;
-  const int64_t row0 = (int64_t)b * sh.num_heads + kv * G;  // first query head row
+  const int nrows = min(16, sh.rows - tile * 16);  // query rows of this tile
 
-  const int seq = clamped_len(seq_lens, b, sh, status, split == 0 && kv == 0 && tid == 0);
+  const int seq = clamped_len(seq_lens, b, sh, status, split == 0 && blockIdx.x == 0 && tid == 0);
   if (seq <= 0) {
     // Empty sequence: defined as a zero output.
     if (split == 0)
-      for (int e = tid; e < G * (D / 4); e += 64 * NW)
-        store_bf16x4(out + (row0 + e / (D / 4)) * D + 4 * (e % (D / 4)), f32x4{0.f, 0.f, 0.f, 0.f});
+      for (int e = tid; e < nrows * (D / 4); e += 64 * NW)
+        store_bf16x4(out + (row_base(b, kv, sh) + row_offset(tile * 16 + e / (D / 4), sh)) * D +
+                         4 * (e % (D / 4)),
+                     f32x4{0.f, 0.f, 0.f, 0.f});
     return;
   }
   const int t0 = split * sh.tokens_per_split;
   if (t0 >= seq) return;  // uniform over the workgroup: no barrier is skipped by part of it
   const int t1 = min(t0 + sh.tokens_per_split, seq);
   const bool single = seq <= sh.tokens_per_split;
-  const int n_chunks = (seq + kChunk - 1) / kChunk;
+  const int c_last = (seq - 1) / kChunk;
+  // First chunk any row of this tile must mask (causal), else the last chunk.
+  const int c_mask =
+      kCausal ? min(c_last, max(0, row_key_limit(tile * 16, seq, sh)) / kChunk) : c_last;
 
   bf16x8 qop[D / 32];
-  load_q<D>(qop, q, b, kv, sh, lane);
+  load_q<D>(qop, q, b, kv, tile, sh, lane);
   SoftmaxState<D> st;
-#pragma unroll
-  for (int i = 0; i < D / 16; ++i) st.o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  st.m = -INFINITY;
-  st.l = 0.f;
+  reset_state<D>(st);
   bool bad_page = false;
-  stream_chunks<D, NBUF, NW>(st, qop, kc, vc, block_table + (int64_t)b * sh.max_pages, kv,
-                             t0 / kChunk, (t1 + kChunk - 1) / kChunk, n_chunks - 1,
-                             seq - (n_chunks - 1) * kChunk, wv, L::ktile(lds, wv), sh, bad_page);
+  stream_chunks<D, NBUF, NW, kCausal>(st, qop, kc, vc, block_table + (int64_t)b * sh.max_pages,
+                                      kv, t0 / kChunk, (t1 + kChunk - 1) / kChunk, seq, c_mask,
+                                      row_key_limit(tile * 16 + (lane & 15), seq, sh), wv,
+                                      L::ktile(lds, wv), sh, bad_page);
   if (bad_page && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
   publish_wave_state<D, NW>(lds, st, wv);
-  for (int e = tid; e < G * (D / 4); e += 64 * NW) {
+  for (int e = tid; e < nrows * (D / 4); e += 64 * NW) {
     const int hh = e / (D / 4);
     const int d = 4 * (e - hh * (D / 4));
     float lse;
     const f32x4 o = merged_head<D, NW>(lds, hh, d, lse);
-    const int64_t row = row0 + hh;
+    const int64_t row = row_base(b, kv, sh) + row_offset(tile * 16 + hh, sh);
     if (single) {
       store_bf16x4(out + row * D + d, o);
     } else {
@@ -706,15 +782,15 @@ __device__ __forceinline__ int block_sum(int x, int* sred) {
 }
 
 // One launch of num_groups workgroups covers the whole batch whatever the length mix.  Every
-// (sequence b, KV head kv) "unit" with n_b = ceil(L_b/16) > 0 chunks occupies n_b +
-// unit_overhead consecutive positions of one global line (units in (b, kv) order; the
+// (sequence b, KV head and row tile j) "unit" with n_b = ceil(L_b/16) > 0 chunks occupies n_b +
+// unit_overhead consecutive positions of one global line (units in (b, j) order; the
 // overhead charges the per-unit Q load and pipeline fill); workgroup w owns positions
 // [w*q, (w+1)*q) with q = ceil(total / num_groups), found from seq_lens on the device, so a
 // ragged batch is balanced without the host seeing its lengths.  A unit a workgroup covers
 // entirely is written out as bf16; a unit cut into several pieces has each piece written as
 // a normalised partial (O/l, log2-sum-exp) to its own slot, and the last piece to finish
 // merges them through a fan-in-8 tree of per-unit counters, so the whole call is one launch.
-template <int D, int NBUF, int NW>
+template <int D, int NBUF, int NW, bool kCausal>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     D == 64 ? MX_WAVES_PER_EU_D64 : (D == 128 ? MX_WAVES_PER_EU_D128 : MX_WAVES_PER_EU_D256))))
 void mx_paged_decode_balanced(
@@ -731,18 +807,19 @@ void mx_paged_decode_balanced(
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wg = blockIdx.x;
-  const int G = sh.group;
-  const int Hkv = sh.num_kv_heads;
+  const int TR = sh.tile_rows;                       // rows per partial slot
+  const int UPS = sh.num_kv_heads * sh.row_tiles;    // units per sequence
   const int B = sh.batch;
   const int alpha = sh.unit_overhead;
 
-  // Empty sequences (L <= 0) are defined as zero output; sequence b's zeros are written by
-  // workgroup b % num_groups.
+  // Empty sequences (L <= 0) are defined as zero output; sequence b's zeros (its seqlen_q *
+  // num_heads consecutive rows) are written by workgroup b % num_groups.
   for (int b = wg; b < B; b += sh.num_groups) {
-    if (seq_lens[b] <= 0)
-      for (int e = tid; e < sh.num_heads * (D / 4); e += 64 * NW)
-        store_bf16x4(out + ((int64_t)b * sh.num_heads + e / (D / 4)) * D + 4 * (e % (D / 4)),
-                     f32x4{0.f, 0.f, 0.f, 0.f});
+    if (seq_lens[b] <= 0) {
+      uint16_t* ob = out + (int64_t)b * sh.seqlen_q * sh.num_heads * D;
+      for (int e = tid; e < sh.seqlen_q * sh.num_heads * (D / 4); e += 64 * NW)
+        store_bf16x4(ob + 4 * (int64_t)e, f32x4{0.f, 0.f, 0.f, 0.f});
+    }
   }
 
   // Sequence weights (positions per sequence).  The batch is at most 512 sequences, so every
@@ -751,7 +828,7 @@ void mx_paged_decode_balanced(
   constexpr int kScanPerThread = (512 + 64 * NW - 1) / (64 * NW);
   auto weight = [&](int b, bool report) -> int {
     const int seq = clamped_len(seq_lens, b, sh, status, report);
-    return seq > 0 ? Hkv * ((seq + kChunk - 1) / kChunk + alpha) : 0;
+    return seq > 0 ? UPS * ((seq + kChunk - 1) / kChunk + alpha) : 0;
   };
   int wts[kScanPerThread];
   int mine = 0;
@@ -818,7 +895,7 @@ void mx_paged_decode_balanced(
   int seq = clamped_len(seq_lens, b, sh, status, false);
   int n_b = (seq + kChunk - 1) / kChunk;
   int span = n_b + alpha;
-  int j = (x_begin - seq_start) / span;  // head slot of the unit in position order
+  int j = (x_begin - seq_start) / span;  // (KV head, row tile) of the unit
   int u0 = seq_start + j * span;  // first position of unit (b, j)
   const int per_level = kMaxSlots;  // counters of merge level l start at l * kMaxSlots
   bool bad_page = false;
@@ -829,30 +906,35 @@ void mx_paged_decode_balanced(
     const int ca = max(x_begin, cpos) - cpos;
     const int cb = min(x_end, cpos + n_b) - cpos;
     if (ca < cb) {
-      const int unit = b * Hkv + j;
-      const int kv = j;
+      const int unit = b * UPS + j;
+      const int kv = sh.row_tiles == 1 ? j : j / sh.row_tiles;
+      const int tile = j - kv * sh.row_tiles;
+      const int nrows = min(16, sh.rows - tile * 16);
+      const int64_t rbase = row_base(b, kv, sh);
       const int first_wg = cpos / qsz;
       const int npieces = (cpos + n_b - 1) / qsz - first_wg + 1;
-      const int64_t row0 = (int64_t)b * sh.num_heads + kv * G;
+      const int c_last = n_b - 1;
+      const int c_mask =
+          kCausal ? min(c_last, max(0, row_key_limit(tile * 16, seq, sh)) / kChunk) : c_last;
 
       bf16x8 qop[D / 32];
-      load_q<D>(qop, q, b, kv, sh, lane);
+      load_q<D>(qop, q, b, kv, tile, sh, lane);
       SoftmaxState<D> st;
-#pragma unroll
-      for (int i = 0; i < D / 16; ++i) st.o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-      st.m = -INFINITY;
-      st.l = 0.f;
-      stream_chunks<D, NBUF, NW>(st, qop, kc, vc, block_table + (int64_t)b * sh.max_pages, kv,
-                                 ca, cb, n_b - 1, seq - (n_b - 1) * kChunk, wv,
-                                 L::ktile(lds, wv), sh, bad_page);
+      reset_state<D>(st);
+      stream_chunks<D, NBUF, NW, kCausal>(st, qop, kc, vc,
+                                          block_table + (int64_t)b * sh.max_pages, kv, ca, cb,
+                                          seq, c_mask,
+                                          row_key_limit(tile * 16 + (lane & 15), seq, sh), wv,
+                                          L::ktile(lds, wv), sh, bad_page);
       publish_wave_state<D, NW>(lds, st, wv);
 
       if (npieces == 1) {
-        for (int e = tid; e < G * (D / 4); e += 64 * NW) {
+        for (int e = tid; e < nrows * (D / 4); e += 64 * NW) {
           const int hh = e / (D / 4);
           const int d = 4 * (e - hh * (D / 4));
           float lse;
-          store_bf16x4(out + (row0 + hh) * D + d, merged_head<D, NW>(lds, hh, d, lse));
+          store_bf16x4(out + (rbase + row_offset(tile * 16 + hh, sh)) * D + d,
+                       merged_head<D, NW>(lds, hh, d, lse));
         }
       } else {
         // Piece k of the unit goes to slot slot0 + k; level-l item j of the merge tree covers
@@ -860,9 +942,9 @@ void mx_paged_decode_balanced(
         const int slot0 = first_wg + unit;
         int item = wg - first_wg;
         {
-          float* po = part_o + (int64_t)(slot0 + item) * G * D;
-          float* pl = part_lse + (int64_t)(slot0 + item) * G;
-          for (int e = tid; e < G * (D / 4); e += 64 * NW) {
+          float* po = part_o + (int64_t)(slot0 + item) * TR * D;
+          float* pl = part_lse + (int64_t)(slot0 + item) * TR;
+          for (int e = tid; e < nrows * (D / 4); e += 64 * NW) {
             const int hh = e / (D / 4);
             const int d = 4 * (e - hh * (D / 4));
             float lse;
@@ -889,7 +971,7 @@ void mx_paged_decode_balanced(
           acquire_partials();
           const int nnext = (nitems + kMergeFanIn - 1) / kMergeFanIn;
           // Merge items grp*8 .. grp*8+gsize-1 (slots gslot + t*stride).
-          for (int e = tid; e < G * (D / 4); e += 64 * NW) {
+          for (int e = tid; e < nrows * (D / 4); e += 64 * NW) {
             const int hh = e / (D / 4);
             const int d = 4 * (e - hh * (D / 4));
             float mx = -INFINITY;
@@ -899,32 +981,36 @@ void mx_paged_decode_balanced(
 #pragma unroll
             for (int t = 0; t < kMergeFanIn; ++t) {
               const int64_t sl = gslot + t * stride;
-              lses[t] = t < gsize ? load_partial1(part_lse + sl * G + hh) : -INFINITY;
-              vals[t] = t < gsize ? load_partial4(part_o + (sl * G + hh) * D + d)
+              lses[t] = t < gsize ? load_partial1(part_lse + sl * TR + hh) : -INFINITY;
+              vals[t] = t < gsize ? load_partial4(part_o + (sl * TR + hh) * D + d)
                                   : f32x4{0.f, 0.f, 0.f, 0.f};
             }
 #pragma unroll
             for (int t = 0; t < kMergeFanIn; ++t) mx = fmaxf(mx, lses[t]);
+            // A row no piece of the group saw a key for (every lse -inf) stays zeros with
+            // log2-sum-exp -inf: its weights are exp2(-inf) = 0 against a reference of 0.
+            const bool seen = mx > -INFINITY;
+            const float mref = seen ? mx : 0.f;
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
             float wsum = 0.f;
 #pragma unroll
             for (int t = 0; t < kMergeFanIn; ++t) {
-              const float w = __builtin_amdgcn_exp2f(lses[t] - mx);  // 0 for t >= gsize
+              const float w = __builtin_amdgcn_exp2f(lses[t] - mref);  // 0 for t >= gsize
               wsum += w;
               acc += w * vals[t];
             }
-            acc *= 1.0f / wsum;
+            acc *= seen ? 1.0f / wsum : 0.f;
             if (nnext == 1) {
-              store_bf16x4(out + (row0 + hh) * D + d, acc);
+              store_bf16x4(out + (rbase + row_offset(tile * 16 + hh, sh)) * D + d, acc);
             } else {
-              store_partial4(part_o + ((int64_t)gslot * G + hh) * D + d, acc);
-              if (d == 0) s_lse[hh] = mx + log2f(wsum);
+              store_partial4(part_o + ((int64_t)gslot * TR + hh) * D + d, acc);
+              if (d == 0) s_lse[hh] = seen ? mx + log2f(wsum) : -INFINITY;
             }
           }
           if (nnext == 1) break;
           // Every thread has read the group's log-sum-exps before any is overwritten.
           __syncthreads();
-          if (tid < G) store_partial1(part_lse + (int64_t)gslot * G + tid, s_lse[tid]);
+          if (tid < nrows) store_partial1(part_lse + (int64_t)gslot * TR + tid, s_lse[tid]);
           item = grp;
           nitems = nnext;
           stride *= kMergeFanIn;
@@ -937,7 +1023,7 @@ void mx_paged_decode_balanced(
     // Next unit.
     u0 += span;
     if (u0 >= x_end) break;
-    if (++j == Hkv) {
+    if (++j == UPS) {
       j = 0;
       seq = 0;
       while (seq <= 0 && ++b < B) seq = clamped_len(seq_lens, b, sh, status, false);
@@ -950,23 +1036,26 @@ void mx_paged_decode_balanced(
 }
 
 // ------------------------------------------------------------------------------------------
-// Combine kernel: out[b, h] = sum_s 2^(lse_s - M) * O_s / sum_s 2^(lse_s - M), M = max_s lse_s
-// over the splits that hold tokens of sequence b (optimized_c500_flash_attn.cu:666-728).
+// Combine kernel: out[row] = sum_s 2^(lse_s - M) * O_s / sum_s 2^(lse_s - M), M = max_s lse_s
+// over the splits that hold tokens of the row's sequence (optimized_c500_flash_attn.cu:666-728);
+// splits in which a causal row saw no key carry lse -inf (weight 0), and a row that saw none at
+// all is written as zeros.
 // ------------------------------------------------------------------------------------------
 
 template <int D>
 __global__ __launch_bounds__(64) void mx_paged_decode_combine(
     const float* __restrict__ part_o, const float* __restrict__ part_lse,
     const int32_t* __restrict__ seq_lens, uint16_t* __restrict__ out, int num_heads,
-    int num_splits, int tokens_per_split, int cap_tokens) {
+    int seqlen_q, int num_splits, int tokens_per_split, int cap_tokens) {
   constexpr int E = D / 64;  // output dims per lane
   const int h = blockIdx.x;
-  const int b = blockIdx.y;
+  const int bt = blockIdx.y;  // sequence * seqlen_q + query token
+  const int b = bt / seqlen_q;
   const int lane = threadIdx.x;
   int seq = min(seq_lens[b], cap_tokens);
   if (seq <= tokens_per_split) return;  // single split (or empty): main kernel wrote it
   const int nsv = (seq + tokens_per_split - 1) / tokens_per_split;
-  const int64_t row = (int64_t)b * num_heads + h;
+  const int64_t row = (int64_t)bt * num_heads + h;
   const float* lse = part_lse + row * num_splits;
   const float* po = part_o + row * num_splits * D + E * lane;
 
@@ -979,6 +1068,10 @@ __global__ __launch_bounds__(64) void mx_paged_decode_combine(
 #pragma unroll
   for (int e = 0; e < E; ++e) acc[e] = 0.f;
   float wsum = 0.f;
+  if (mx == -INFINITY) {
+    mx = 0.f;      // no split saw a key: every weight below is 0
+    wsum = 1.f;    // and the output zeros
+  }
 #pragma unroll 4
   for (int s = 0; s < nsv; ++s) {
     const float w = __builtin_amdgcn_exp2f(lse[s] - mx);
@@ -1055,14 +1148,16 @@ int64_t groups_per_cu(int64_t head_dim) { return head_dim == 64 ? 2 : 1; }
 #endif
 constexpr int64_t kBalancedMaxBatch = 512;
 constexpr int64_t kBalancedMaxGroups = 4095;  // pieces per unit stay within the 8^4 merge tree
-constexpr int64_t kBalancedMaxUnits = 8192;   // batch * Hkv (fixed counter region)
+constexpr int64_t kBalancedMaxUnits = 8192;   // batch * Hkv * row tiles (counter region)
 
 struct Plan {
   int schedule = MX_SCHEDULE_SPLIT_GRID;
   int64_t splits = 1;             // split grid: splits per sequence
   int64_t tokens_per_split = 0;   // split grid
   int64_t groups = 0;             // balanced: workgroups of the launch
-  int64_t slots = 0;              // balanced: partial slots (groups + batch * Hkv)
+  int64_t slots = 0;              // balanced: partial slots (groups + units)
+  int64_t rows = 1;               // query rows per KV head: seqlen_q * group
+  int64_t row_tiles = 1;          // ceil(rows / 16)
   int64_t cap_tokens = 0;
   int64_t counter_offset = 0;
   int64_t lse_offset = 0;
@@ -1095,14 +1190,14 @@ int query_num_cus(int64_t* num_cus) {
 }
 
 // Validates the shape and computes the split plan.  Performs no HIP call when num_cus > 0.
-int make_plan(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
-              int64_t page_size, int64_t max_pages, int64_t max_seq_len, int64_t num_splits,
-              int64_t num_cus, Plan* plan) {
-  if (batch < 1 || num_heads < 1 || num_kv_heads < 1 || head_dim < 1 || page_size < 1 ||
-      max_pages < 1)
+int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads,
+              int64_t head_dim, int64_t page_size, int64_t max_pages, int64_t max_seq_len,
+              int64_t num_splits, int64_t num_cus, Plan* plan) {
+  if (batch < 1 || seqlen_q < 1 || num_heads < 1 || num_kv_heads < 1 || head_dim < 1 ||
+      page_size < 1 || max_pages < 1)
     return fail(MX_STATUS_INVALID_SHAPE,
-                "batch, num_heads, num_kv_heads, head_dim, page_size and max_pages_per_seq "
-                "must all be >= 1");
+                "batch, seqlen_q, num_heads, num_kv_heads, head_dim, page_size and "
+                "max_pages_per_seq must all be >= 1");
   if (num_heads % num_kv_heads != 0)
     return fail(MX_STATUS_INVALID_SHAPE, "num_heads must be a multiple of num_kv_heads");
   if (num_heads / num_kv_heads > 16)
@@ -1113,6 +1208,16 @@ int make_plan(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t he
       page_size != 256)
     return fail(MX_STATUS_UNSUPPORTED, "page_size must be 16, 32, 64, 128 or 256");
   if (batch > kMaxGridDim) return fail(MX_STATUS_UNSUPPORTED, "batch must be <= 65535");
+  if (batch * seqlen_q > kMaxGridDim)
+    return fail(MX_STATUS_UNSUPPORTED, "batch * seqlen_q must be <= 65535");
+  const int64_t group = num_heads / num_kv_heads;
+  const int64_t rows = seqlen_q * group;
+  const int64_t row_tiles = ceil_div(rows, 16);
+  const int64_t tile_rows = std::min<int64_t>(rows, 16);
+  if (num_kv_heads * row_tiles > kMaxGridDim)
+    return fail(MX_STATUS_UNSUPPORTED, "num_kv_heads * ceil(seqlen_q * group / 16) must be <= 65535");
+  plan->rows = rows;
+  plan->row_tiles = row_tiles;
   if (num_heads > kMaxGridDim) return fail(MX_STATUS_UNSUPPORTED, "num_heads must be <= 65535");
   if (max_pages > (int64_t)INT32_MAX / page_size)
     return fail(MX_STATUS_UNSUPPORTED, "max_pages_per_seq * page_size must fit in int32");
@@ -1132,7 +1237,7 @@ int make_plan(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t he
       const int st = query_num_cus(&num_cus);
       if (st != MX_STATUS_OK) return st;
     }
-    const int64_t units = batch * num_kv_heads;
+    const int64_t units = batch * num_kv_heads * row_tiles;
     ns = ceil_div(num_cus * groups_per_cu(head_dim), units);
     const int64_t max_by_len = ceil_div(cap, kMinTokensPerSplit);
     if (ns > max_by_len) ns = max_by_len;
@@ -1151,8 +1256,9 @@ int make_plan(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t he
   int shift = 0;
   while ((int64_t(kChunk) << shift) < page_size) ++shift;
   plan->chunk_shift = shift;
-  const bool balanced_ok = batch <= kBalancedMaxBatch && batch * num_kv_heads <= kBalancedMaxUnits;
-  const bool balanced_auto = num_splits == 0 && balanced_ok && batch * num_kv_heads >= kBalancedMinUnits;
+  const int64_t units = batch * num_kv_heads * row_tiles;
+  const bool balanced_ok = batch <= kBalancedMaxBatch && units <= kBalancedMaxUnits;
+  const bool balanced_auto = num_splits == 0 && balanced_ok && units >= kBalancedMinUnits;
   if ((num_splits < 0 && balanced_ok) || balanced_auto) {
     // Length-balanced single launch (automatic, or num_splits < 0 = that many workgroups).
     int64_t groups;
@@ -1166,27 +1272,27 @@ int make_plan(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t he
       groups = num_cus * groups_per_cu(head_dim);
     }
     if (groups > kBalancedMaxGroups) groups = kBalancedMaxGroups;
-    const int64_t group = num_heads / num_kv_heads;
     plan->schedule = MX_SCHEDULE_BALANCED;
     plan->splits = 0;
     plan->tokens_per_split = 0;
     plan->groups = groups;
-    plan->slots = groups + batch * num_kv_heads;
+    plan->slots = groups + units;
     plan->cap_tokens = cap;
     plan->counter_offset = kStatusBytes;
     plan->lse_offset = kPartialBase;
-    plan->o_offset = plan->lse_offset + align_up(plan->slots * group * 4, 256);
-    plan->workspace_bytes = plan->o_offset + plan->slots * group * head_dim * 4;
+    plan->o_offset = plan->lse_offset + align_up(plan->slots * tile_rows * 4, 256);
+    plan->workspace_bytes = plan->o_offset + plan->slots * tile_rows * head_dim * 4;
     return MX_STATUS_OK;
   }
   if (num_splits < 0)
     return fail(MX_STATUS_UNSUPPORTED,
-                "the balanced schedule supports batch <= 512 and batch * num_kv_heads <= 8192");
+                "the balanced schedule supports batch <= 512 and batch * num_kv_heads * "
+                "ceil(seqlen_q * group / 16) <= 8192");
   if (ns > 1) {
-    const int64_t rows = batch * num_heads * ns;
+    const int64_t prow = batch * seqlen_q * num_heads * ns;
     plan->lse_offset = kPartialBase;
-    plan->o_offset = kPartialBase + align_up(rows * 4, 256);
-    plan->workspace_bytes = plan->o_offset + rows * head_dim * 4;
+    plan->o_offset = kPartialBase + align_up(prow * 4, 256);
+    plan->workspace_bytes = plan->o_offset + prow * head_dim * 4;
   } else {
     plan->lse_offset = plan->o_offset = 0;
     plan->workspace_bytes = kStatusBytes;
@@ -1237,11 +1343,12 @@ int internal_workspace(int64_t need, void** out) {
   return MX_STATUS_OK;
 }
 
-template <int D>
+template <int D, bool kCausal>
 hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v, void* out,
                   const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
-                  int64_t num_heads, int64_t num_kv_heads, int64_t page_size, int64_t num_pages,
-                  int64_t max_pages, float scale, char* ws, int32_t phase, hipStream_t stream) {
+                  int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads, int64_t page_size,
+                  int64_t num_pages, int64_t max_pages, float scale, char* ws, int32_t phase,
+                  hipStream_t stream) {
   constexpr int kNW = waves_per_group<D>();
   constexpr int kNBUF = ring_depth<D>();
   MainShape sh;
@@ -1250,6 +1357,12 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   sh.num_heads = (int)num_heads;
   sh.num_kv_heads = (int)num_kv_heads;
   sh.group = (int)(num_heads / num_kv_heads);
+  sh.group_magic = sh.group == 1 ? 0u : (uint32_t)((1ull << 32) / (uint64_t)sh.group + 1);
+  sh.seqlen_q = (int)seqlen_q;
+  sh.causal = kCausal ? 1 : 0;
+  sh.rows = (int)plan.rows;
+  sh.row_tiles = (int)plan.row_tiles;
+  sh.tile_rows = (int)std::min<int64_t>(plan.rows, 16);
   sh.batch = (int)batch;
   sh.max_pages = (int)max_pages;
   sh.num_pages = (num_pages > 0 && num_pages <= INT32_MAX) ? (int)num_pages : 0;
@@ -1266,7 +1379,8 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   if (plan.schedule == MX_SCHEDULE_BALANCED) {
     // One launch does everything; MX_PHASE_COMBINE_ONLY has nothing left to do.
     if (phase == MX_PHASE_COMBINE_ONLY) return hipSuccess;
-    hipLaunchKernelGGL((mx_paged_decode_balanced<D, kNBUF, kNW>), dim3((unsigned)plan.groups),
+    hipLaunchKernelGGL((mx_paged_decode_balanced<D, kNBUF, kNW, kCausal>),
+                       dim3((unsigned)plan.groups),
                        dim3(64 * kNW), 0, stream, static_cast<const uint16_t*>(q),
                        static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
                        static_cast<uint16_t*>(out), seq_lens, block_table,
@@ -1279,8 +1393,9 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   float* part_lse = plan.splits > 1 ? reinterpret_cast<float*>(ws + plan.lse_offset) : nullptr;
   float* part_o = plan.splits > 1 ? reinterpret_cast<float*>(ws + plan.o_offset) : nullptr;
   if (phase != MX_PHASE_COMBINE_ONLY) {
-    const dim3 grid((unsigned)num_kv_heads, (unsigned)batch, (unsigned)plan.splits);
-    hipLaunchKernelGGL((mx_paged_decode_splitkv<D, kNBUF, kNW>), grid, dim3(64 * kNW), 0,
+    const dim3 grid((unsigned)(num_kv_heads * plan.row_tiles), (unsigned)batch,
+                    (unsigned)plan.splits);
+    hipLaunchKernelGGL((mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal>), grid, dim3(64 * kNW), 0,
                        stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                        static_cast<const uint16_t*>(v), static_cast<uint16_t*>(out), seq_lens,
                        block_table, part_o, part_lse, status, sh);
@@ -1288,10 +1403,10 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
     if (e != hipSuccess) return e;
   }
   if (phase != MX_PHASE_MAIN_ONLY && plan.splits > 1) {
-    const dim3 grid((unsigned)num_heads, (unsigned)batch);
+    const dim3 grid((unsigned)num_heads, (unsigned)(batch * seqlen_q));
     hipLaunchKernelGGL(mx_paged_decode_combine<D>, grid, dim3(64), 0, stream, part_o, part_lse,
-                       seq_lens, static_cast<uint16_t*>(out), (int)num_heads, (int)plan.splits,
-                       (int)plan.tokens_per_split, (int)plan.cap_tokens);
+                       seq_lens, static_cast<uint16_t*>(out), (int)num_heads, (int)seqlen_q,
+                       (int)plan.splits, (int)plan.tokens_per_split, (int)plan.cap_tokens);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -1306,32 +1421,33 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
 
 extern "C" {
 
-int mx_paged_gqa_decode_plan(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
-                             int64_t head_dim, int64_t page_size, int64_t max_pages_per_seq,
-                             int64_t max_seq_len, int64_t num_splits, int64_t num_cus,
-                             int64_t* schedule_out, int64_t* splits_out,
+int mx_paged_gqa_decode_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads,
+                             int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                             int64_t max_pages_per_seq, int64_t max_seq_len, int64_t num_splits,
+                             int64_t num_cus, int64_t* schedule_out, int64_t* splits_out,
                              int64_t* tokens_per_split_out, int64_t* workgroups_out,
                              int64_t* workspace_bytes_out) {
   Plan plan;
-  const int st = make_plan(batch, num_heads, num_kv_heads, head_dim, page_size,
+  const int st = make_plan(batch, seqlen_q, num_heads, num_kv_heads, head_dim, page_size,
                            max_pages_per_seq, max_seq_len, num_splits, num_cus, &plan);
   if (st != MX_STATUS_OK) return st;
   if (schedule_out) *schedule_out = plan.schedule;
   if (splits_out) *splits_out = plan.splits;
   if (tokens_per_split_out) *tokens_per_split_out = plan.tokens_per_split;
   if (workgroups_out)
-    *workgroups_out = plan.schedule == MX_SCHEDULE_BALANCED ? plan.groups
-                                                            : batch * num_kv_heads * plan.splits;
+    *workgroups_out = plan.schedule == MX_SCHEDULE_BALANCED
+                          ? plan.groups
+                          : batch * num_kv_heads * plan.row_tiles * plan.splits;
   if (workspace_bytes_out) *workspace_bytes_out = plan.workspace_bytes;
   return ok();
 }
 
-int64_t mx_paged_gqa_decode_workspace_size(int64_t batch, int64_t num_heads,
+int64_t mx_paged_gqa_decode_workspace_size(int64_t batch, int64_t seqlen_q, int64_t num_heads,
                                            int64_t num_kv_heads, int64_t head_dim,
                                            int64_t page_size, int64_t max_pages_per_seq,
                                            int64_t max_seq_len, int64_t num_splits) {
   Plan plan;
-  const int st = make_plan(batch, num_heads, num_kv_heads, head_dim, page_size,
+  const int st = make_plan(batch, seqlen_q, num_heads, num_kv_heads, head_dim, page_size,
                            max_pages_per_seq, max_seq_len, num_splits, 0, &plan);
   if (st != MX_STATUS_OK) return st;
   ok();
@@ -1340,20 +1456,22 @@ int64_t mx_paged_gqa_decode_workspace_size(int64_t batch, int64_t num_heads,
 
 int mx_paged_gqa_decode(const void* q, const void* k_cache, const void* v_cache, void* out,
                         const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
-                        int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
-                        int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
-                        int64_t max_seq_len, float scale, int64_t num_splits, void* workspace,
-                        int64_t workspace_bytes, int32_t phase, void* stream) {
+                        int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads,
+                        int64_t head_dim, int64_t page_size, int64_t num_pages,
+                        int64_t max_pages_per_seq, int64_t max_seq_len, int32_t causal,
+                        float scale, int64_t num_splits, void* workspace, int64_t workspace_bytes,
+                        int32_t phase, void* stream) {
   if (!q || !k_cache || !v_cache || !out || !seq_lens || !block_table)
     return fail(MX_STATUS_NULL_POINTER,
                 "q, k_cache, v_cache, out, seq_lens and block_table must be non-NULL");
   if (phase != 0 && phase != MX_PHASE_MAIN_ONLY && phase != MX_PHASE_COMBINE_ONLY)
     return fail(MX_STATUS_INVALID_ARGUMENT, "phase must be 0, 1 or 2");
+  if (causal != 0 && causal != 1) return fail(MX_STATUS_INVALID_ARGUMENT, "causal must be 0 or 1");
   if (!std::isfinite(scale)) return fail(MX_STATUS_INVALID_ARGUMENT, "scale must be finite");
   if (num_pages < 0) return fail(MX_STATUS_INVALID_SHAPE, "num_pages must be >= 0");
   Plan plan;
-  int st = make_plan(batch, num_heads, num_kv_heads, head_dim, page_size, max_pages_per_seq,
-                     max_seq_len, num_splits, 0, &plan);
+  int st = make_plan(batch, seqlen_q, num_heads, num_kv_heads, head_dim, page_size,
+                     max_pages_per_seq, max_seq_len, num_splits, 0, &plan);
   if (st != MX_STATUS_OK) return st;
   if (workspace != nullptr) {
     if (workspace_bytes < plan.workspace_bytes)
@@ -1367,20 +1485,24 @@ int mx_paged_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
   hipStream_t s = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   hipError_t e;
+  // A causal mask changes nothing for a single query token (it sees every key).
+  const bool masked = causal != 0 && seqlen_q > 1;
+#define MX_LAUNCH(DIM, CAUSAL)                                                                \
+  launch<DIM, CAUSAL>(plan, q, k_cache, v_cache, out, seq_lens, block_table, batch, seqlen_q,  \
+                      num_heads, num_kv_heads, page_size, num_pages, max_pages_per_seq, scale, \
+                      ws, phase, s)
   switch (head_dim) {
     case 64:
-      e = launch<64>(plan, q, k_cache, v_cache, out, seq_lens, block_table, batch, num_heads,
-                     num_kv_heads, page_size, num_pages, max_pages_per_seq, scale, ws, phase, s);
+      e = masked ? MX_LAUNCH(64, true) : MX_LAUNCH(64, false);
       break;
     case 128:
-      e = launch<128>(plan, q, k_cache, v_cache, out, seq_lens, block_table, batch, num_heads,
-                      num_kv_heads, page_size, num_pages, max_pages_per_seq, scale, ws, phase, s);
+      e = masked ? MX_LAUNCH(128, true) : MX_LAUNCH(128, false);
       break;
     default:
-      e = launch<256>(plan, q, k_cache, v_cache, out, seq_lens, block_table, batch, num_heads,
-                      num_kv_heads, page_size, num_pages, max_pages_per_seq, scale, ws, phase, s);
+      e = masked ? MX_LAUNCH(256, true) : MX_LAUNCH(256, false);
       break;
   }
+#undef MX_LAUNCH
   if (e != hipSuccess)
     return fail(MX_STATUS_HIP_ERROR, std::string("kernel launch failed: ") + hipGetErrorString(e));
   return ok();
@@ -1392,10 +1514,10 @@ void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_pa
                 int64_t num_heads_k, int64_t headdim, int64_t page_block_size,
                 int64_t num_blocks, int64_t causal) {
   int st;
-  if (seqlen_q != 1) {
-    st = fail(MX_STATUS_UNSUPPORTED, "run_kernel: seqlen_q must be 1 (decode)");
-  } else if (causal != 0) {
-    st = fail(MX_STATUS_UNSUPPORTED, "run_kernel: causal must be 0");
+  if (seqlen_q < 1) {
+    st = fail(MX_STATUS_INVALID_SHAPE, "run_kernel: seqlen_q must be >= 1");
+  } else if (causal != 0 && causal != 1) {
+    st = fail(MX_STATUS_INVALID_ARGUMENT, "run_kernel: causal must be 0 or 1");
   } else if (batch_size < 1 || num_blocks < batch_size || num_blocks % batch_size != 0) {
     st = fail(MX_STATUS_INVALID_SHAPE,
               "run_kernel: num_blocks must be a positive multiple of batch_size");
@@ -1408,9 +1530,9 @@ void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_pa
     // The legacy ABI carries no pool size (num_blocks is the table row width times batch),
     // so only negative page ids are flagged.
     st = mx_paged_gqa_decode(q, k_cache_paged, v_cache_paged, output, cache_seqlens,
-                             block_table, batch_size, num_heads, num_heads_k, headdim,
-                             page_block_size, 0, num_blocks / batch_size, seqlen_k, scale, 0,
-                             nullptr, 0, 0, nullptr);
+                             block_table, batch_size, seqlen_q, num_heads, num_heads_k, headdim,
+                             page_block_size, 0, num_blocks / batch_size, seqlen_k,
+                             (int32_t)causal, scale, 0, nullptr, 0, 0, nullptr);
   }
   if (st != MX_STATUS_OK) fprintf(stderr, "run_kernel: %s\n", g_last_error.c_str());
 }

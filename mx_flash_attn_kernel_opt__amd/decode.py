@@ -34,7 +34,7 @@ def _stream_handle(stream, device: torch.device) -> ctypes.c_void_p:
 
 def plan(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
          max_pages_per_seq: int, max_seq_len: int = 0, num_splits: int = 0,
-         num_cus: int = 0) -> dict:
+         num_cus: int = 0, seqlen_q: int = 1) -> dict:
     """Split plan of a call (host only when ``num_cus`` > 0).
 
     Returns ``{"schedule", "splits", "tokens_per_split", "workgroups", "workspace_bytes"}``
@@ -43,8 +43,9 @@ def plan(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, page_size
     """
     lib = _lib.load()
     sch, ns, tps, wgs, ws = (ctypes.c_int64() for _ in range(5))
-    st = lib.mx_paged_gqa_decode_plan(batch, num_heads, num_kv_heads, head_dim, page_size,
-                                      max_pages_per_seq, max_seq_len, num_splits, num_cus,
+    st = lib.mx_paged_gqa_decode_plan(batch, seqlen_q, num_heads, num_kv_heads, head_dim,
+                                      page_size, max_pages_per_seq, max_seq_len, num_splits,
+                                      num_cus,
                                       ctypes.byref(sch), ctypes.byref(ns), ctypes.byref(tps),
                                       ctypes.byref(wgs), ctypes.byref(ws))
     _lib.check(st)
@@ -55,10 +56,10 @@ def plan(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, page_size
 
 def workspace_size(batch: int, num_heads: int, num_kv_heads: int, head_dim: int,
                    page_size: int, max_pages_per_seq: int, max_seq_len: int = 0,
-                   num_splits: int = 0) -> int:
+                   num_splits: int = 0, seqlen_q: int = 1) -> int:
     n = _lib.load().mx_paged_gqa_decode_workspace_size(
-        batch, num_heads, num_kv_heads, head_dim, page_size, max_pages_per_seq, max_seq_len,
-        num_splits)
+        batch, seqlen_q, num_heads, num_kv_heads, head_dim, page_size, max_pages_per_seq,
+        max_seq_len, num_splits)
     if n < 0:
         _lib.check(int(n))
     return int(n)
@@ -69,17 +70,27 @@ def make_workspace(nbytes: int, device) -> torch.Tensor:
     return torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
+def _query_shape(q: torch.Tensor) -> tuple[int, int, int, int]:
+    """(B, seqlen_q, Hq, D) of a [B, Hq, D] or [B, seqlen_q, Hq, D] query."""
+    if q.dim() == 3:
+        return q.shape[0], 1, q.shape[1], q.shape[2]
+    _require(q.dim() == 4, "q must be [B, Hq, D] or [B, seqlen_q, Hq, D]")
+    return tuple(q.shape)
+
+
 def paged_gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                      block_table: torch.Tensor, seq_lens: torch.Tensor,
                      scale: float | None = None, *, out: torch.Tensor | None = None,
-                     num_splits: int = 0, max_seq_len: int = 0,
+                     causal: bool = False, num_splits: int = 0, max_seq_len: int = 0,
                      workspace: torch.Tensor | None = None, phase: int = 0,
                      stream=None) -> torch.Tensor:
-    """out[b, h] = softmax(q[b, h] . K_b^T * scale) . V_b over the first seq_lens[b] tokens.
+    """out[b, i, h] = softmax(q[b, i, h] . K_b^T * scale) . V_b over the first seq_lens[b]
+    tokens (with ``causal``, query token i of seqlen_q sees keys t < L - seqlen_q + i + 1).
 
-    q: [B, Hq, D] or [B, 1, Hq, D] bf16; k_cache / v_cache: [num_pages, page_size, Hkv, D]
-    bf16; block_table: [B, max_pages] int32; seq_lens: [B] int32; all on one GPU, contiguous.
-    ``scale`` defaults to 1/sqrt(D) (reference submission_clean.cu:451).
+    q: [B, Hq, D] (one query token) or [B, seqlen_q, Hq, D] bf16; k_cache / v_cache:
+    [num_pages, page_size, Hkv, D] bf16; block_table: [B, max_pages] int32; seq_lens: [B] int32;
+    all on one GPU, contiguous.  ``scale`` defaults to 1/sqrt(D) (reference
+    submission_clean.cu:451).
     """
     _require(q.is_cuda, "q must be a device tensor")
     dev = q.device
@@ -90,13 +101,7 @@ def paged_gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
         _require(t.device == dev, f"{name} must be on {dev}")
         _require(t.dtype == dt, f"{name} must be {dt}, got {t.dtype}")
         _require(t.is_contiguous(), f"{name} must be contiguous")
-    if q.dim() == 4:
-        _require(q.shape[1] == 1, "only one query token per sequence (seqlen_q == 1)")
-        q3 = q.view(q.shape[0], q.shape[2], q.shape[3])
-    else:
-        _require(q.dim() == 3, "q must be [B, Hq, D] or [B, 1, Hq, D]")
-        q3 = q
-    B, Hq, D = q3.shape
+    B, SQ, Hq, D = _query_shape(q)
     _require(k_cache.dim() == 4 and k_cache.shape == v_cache.shape,
              "k_cache and v_cache must both be [num_pages, page_size, Hkv, D]")
     num_pages, P, Hkv, Dk = k_cache.shape
@@ -119,10 +124,10 @@ def paged_gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     lib = _lib.load()
     with torch.cuda.device(dev):
         st = lib.mx_paged_gqa_decode(
-            _ptr(q3), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(seq_lens),
-            _ptr(block_table), B, Hq, Hkv, D, P, num_pages, block_table.shape[1], max_seq_len,
-            float(scale), num_splits, _ptr(workspace), ws_bytes, phase,
-            _stream_handle(stream, dev))
+            _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(seq_lens),
+            _ptr(block_table), B, SQ, Hq, Hkv, D, P, num_pages, block_table.shape[1],
+            max_seq_len, int(bool(causal)), float(scale), num_splits, _ptr(workspace), ws_bytes,
+            phase, _stream_handle(stream, dev))
     _lib.check(st)
     return out
 
@@ -135,23 +140,25 @@ class BoundDecode:
     """
 
     def __init__(self, q, k_cache, v_cache, block_table, seq_lens, scale=None, *, out=None,
-                 num_splits: int = 0, max_seq_len: int = 0, workspace=None, stream=None):
+                 causal: bool = False, num_splits: int = 0, max_seq_len: int = 0,
+                 workspace=None, stream=None):
         # validate once through the tensor-level entry (phase 0 runs a real call)
         self.out = paged_gqa_decode(q, k_cache, v_cache, block_table, seq_lens, scale, out=out,
-                                    num_splits=num_splits, max_seq_len=max_seq_len,
-                                    workspace=workspace, stream=stream)
-        q3 = q.view(q.shape[0], q.shape[2], q.shape[3]) if q.dim() == 4 else q
-        B, Hq, D = q3.shape
+                                    causal=causal, num_splits=num_splits,
+                                    max_seq_len=max_seq_len, workspace=workspace, stream=stream)
+        B, SQ, Hq, D = _query_shape(q)
         num_pages, P, Hkv, _ = k_cache.shape
         if scale is None:
             scale = 1.0 / math.sqrt(D)
-        self.plan = plan(B, Hq, Hkv, D, P, block_table.shape[1], max_seq_len, num_splits)
-        self._keep = (q3, k_cache, v_cache, block_table, seq_lens, workspace)
+        self.plan = plan(B, Hq, Hkv, D, P, block_table.shape[1], max_seq_len, num_splits,
+                         seqlen_q=SQ)
+        self._keep = (q, k_cache, v_cache, block_table, seq_lens, workspace)
         ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
         self._fn = _lib.load().mx_paged_gqa_decode
-        self._args = [_ptr(q3), _ptr(k_cache), _ptr(v_cache), _ptr(self.out), _ptr(seq_lens),
-                      _ptr(block_table), B, Hq, Hkv, D, P, num_pages, block_table.shape[1],
-                      max_seq_len, float(scale), num_splits, _ptr(workspace), ws_bytes]
+        self._args = [_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(self.out), _ptr(seq_lens),
+                      _ptr(block_table), B, SQ, Hq, Hkv, D, P, num_pages, block_table.shape[1],
+                      max_seq_len, int(bool(causal)), float(scale), num_splits, _ptr(workspace),
+                      ws_bytes]
         self._stream = _stream_handle(stream, q.device)
 
     @property

@@ -42,6 +42,8 @@ class DecodeSpec:
     k_scale: float = 1.0
     table: str = "shuffle"         # shuffle | arange
     description: str = ""
+    seqlen_q: int = 1              # query tokens per sequence (q is [B, Hq, D] when 1)
+    causal: bool = False           # end-aligned causal mask for seqlen_q > 1
 
     @property
     def group(self) -> int:
@@ -258,7 +260,9 @@ def make_inputs(spec: DecodeSpec | str, seed: int = 0, device="cpu",
         gen = cpu_gen
     else:
         gen = torch.Generator(device=gen_device).manual_seed(seed)
-    q = _randn_bf16((spec.batch, spec.num_heads, spec.head_dim), gen, gen_device, device)
+    q_shape = ((spec.batch, spec.num_heads, spec.head_dim) if spec.seqlen_q == 1 else
+               (spec.batch, spec.seqlen_q, spec.num_heads, spec.head_dim))
+    q = _randn_bf16(q_shape, gen, gen_device, device)
     kv_shape = (spec.num_pages, spec.page_size, spec.num_kv_heads, spec.head_dim)
     k = _randn_bf16(kv_shape, gen, gen_device, device, spec.k_scale)
     v = _randn_bf16(kv_shape, gen, gen_device, device)
@@ -269,11 +273,12 @@ def make_inputs(spec: DecodeSpec | str, seed: int = 0, device="cpu",
 
 def custom_spec(name: str, seq_lens, num_heads: int, num_kv_heads: int, head_dim: int,
                 page_size: int, max_pages: int | None = None, pool_pages: int = 0,
-                table: str = "shuffle", k_scale: float = 1.0) -> DecodeSpec:
+                table: str = "shuffle", k_scale: float = 1.0, seqlen_q: int = 1,
+                causal: bool = False) -> DecodeSpec:
     """Spec with explicit per-sequence lengths (edge-case tests)."""
     lens = [int(x) for x in seq_lens]
     if max_pages is None:
         max_pages = max(1, max(math.ceil(max(L, 1) / page_size) for L in lens))
     return DecodeSpec(name, len(lens), num_heads, num_kv_heads, head_dim, page_size, max_pages,
                       "explicit", tuple(lens), pool_pages=pool_pages, table=table,
-                      k_scale=k_scale)
+                      k_scale=k_scale, seqlen_q=seqlen_q, causal=causal)

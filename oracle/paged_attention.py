@@ -7,6 +7,10 @@ Reference semantics (file:line in the reference tree):
     block_table[b, t // page_size] at offset t % page_size;
   * only the first ceil(L_b / page_size) table entries are valid (task.md:8-10, 61, 92);
   * scale defaults to 1/sqrt(head_dim) (submission_clean.cu:451);
+  * multi-token queries: q / out [B, seqlen_q, Hq, D] (task.md:56, 59); with causal
+    (task.md:53) query token i sees keys t < L - seqlen_q + i + 1, the end-aligned mask of the
+    reference's oracle flash_attn_with_kvcache (verify_real.py:40-41); a query row that sees no
+    key is defined as zeros;
   * split ranges and the LSE merge: optimized_c500_flash_attn.cu:537-551 and :666-728,
     submission_c500_regions.py:704-731.
 """
@@ -39,67 +43,87 @@ def _gather_sequence(k_cache, v_cache, block_table, b: int, L: int):
     return k.float(), v.float()
 
 
-def paged_decode_reference(q, k_cache, v_cache, block_table, seq_lens, scale=None,
-                           batches=None) -> torch.Tensor:
-    """fp32 restatement of task.md:138-148 on CPU tensors; returns fp32 [B, Hq, D].
+def _visible(L: int, sq: int, causal: bool) -> np.ndarray:
+    """[sq, L] bool: key t is visible to query token i (end-aligned causal mask)."""
+    t = np.arange(L)[None, :]
+    i = np.arange(sq)[:, None]
+    return (t < L - sq + i + 1) if causal else np.ones((sq, L), dtype=bool)
 
-    One sequence at a time: gather its valid pages, upcast to fp32, softmax(q k^T scale) v with
-    query head h reading KV head h // group.  Empty sequences (L <= 0) give zeros.
-    ``batches`` restricts the computation to some sequences (others stay zero).
+
+def paged_decode_reference(q, k_cache, v_cache, block_table, seq_lens, scale=None,
+                           batches=None, causal: bool = False) -> torch.Tensor:
+    """fp32 restatement of task.md:138-148 on CPU tensors; returns fp32 of q's shape.
+
+    q is [B, Hq, D] (one query token) or [B, seqlen_q, Hq, D].  One sequence at a time: gather
+    its valid pages, upcast to fp32, softmax(q k^T scale) v with query head h reading KV head
+    h // group, masked per query token when ``causal``.  Empty sequences (L <= 0) and query
+    rows that see no key give zeros.  ``batches`` restricts the computation to some sequences
+    (others stay zero).
     """
-    q3 = _as3(q)
-    B, Hq, D = q3.shape
+    q4 = q if q.dim() == 4 else q.unsqueeze(1)
+    B, SQ, Hq, D = q4.shape
     Hkv = k_cache.shape[2]
     G = Hq // Hkv
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     lens = torch.as_tensor(seq_lens).cpu()
-    out = torch.zeros(B, Hq, D, dtype=torch.float32)
+    out = torch.zeros(B, SQ, Hq, D, dtype=torch.float32)
     for b in (range(B) if batches is None else batches):
         L = int(lens[b])
         if L <= 0:
             continue
         k, v = _gather_sequence(k_cache, v_cache, block_table, b, L)   # [L, Hkv, D]
-        qb = q3[b].float().view(Hkv, G, D)                             # [Hkv, G, D]
+        qb = q4[b].float().view(SQ, Hkv, G, D).permute(1, 0, 2, 3)     # [Hkv, SQ, G, D]
+        qb = qb.reshape(Hkv, SQ * G, D)
         kt = k.permute(1, 2, 0).contiguous()                           # [Hkv, D, L]
         vt = v.permute(1, 0, 2).contiguous()                           # [Hkv, L, D]
-        logits = torch.matmul(qb, kt) * scale                          # [Hkv, G, L]
-        attn = torch.softmax(logits, dim=-1)
-        out[b] = torch.matmul(attn, vt).reshape(Hq, D)
-    return out
+        logits = torch.matmul(qb, kt) * scale                          # [Hkv, SQ*G, L]
+        vis = torch.from_numpy(np.repeat(_visible(L, SQ, causal), G, axis=0))   # [SQ*G, L]
+        logits = logits.masked_fill(~vis, float("-inf"))
+        attn = torch.softmax(logits, dim=-1).nan_to_num(0.0)           # no visible key -> 0
+        o = torch.matmul(attn, vt)                                     # [Hkv, SQ*G, D]
+        out[b] = o.view(Hkv, SQ, G, D).permute(1, 0, 2, 3).reshape(SQ, Hq, D)
+    return out if q.dim() == 4 else out[:, 0]
 
 
-def paged_decode_fp64(q, k_cache, v_cache, block_table, seq_lens, scale=None) -> np.ndarray:
-    """fp64 numpy brute force, token by token (tiny shapes only).  Returns [B, Hq, D]."""
-    qn = _as3(torch.as_tensor(q)).float().numpy().astype(np.float64)
+def paged_decode_fp64(q, k_cache, v_cache, block_table, seq_lens, scale=None,
+                      causal: bool = False) -> np.ndarray:
+    """fp64 numpy brute force, token by token (tiny shapes only).  Returns q's shape:
+    [B, Hq, D] or [B, seqlen_q, Hq, D]; query token i of seqlen_q sees keys
+    t < L - seqlen_q + i + 1 when ``causal``, and a row with no visible key is zeros."""
+    qt = torch.as_tensor(q)
+    q4 = qt if qt.dim() == 4 else qt.unsqueeze(1)
+    qn = q4.float().numpy().astype(np.float64)
     kn = torch.as_tensor(k_cache).float().numpy().astype(np.float64)
     vn = torch.as_tensor(v_cache).float().numpy().astype(np.float64)
     bt = torch.as_tensor(block_table).numpy()
     lens = torch.as_tensor(seq_lens).numpy()
-    B, Hq, D = qn.shape
+    B, SQ, Hq, D = qn.shape
     P, Hkv = kn.shape[1], kn.shape[2]
     G = Hq // Hkv
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    out = np.zeros((B, Hq, D), dtype=np.float64)
+    out = np.zeros((B, SQ, Hq, D), dtype=np.float64)
     for b in range(B):
         L = int(lens[b])
-        if L <= 0:
-            continue
-        for h in range(Hq):
-            kvh = h // G
-            logits = np.empty(L)
-            for t in range(L):
-                page, off = int(bt[b, t // P]), t % P
-                logits[t] = float(np.dot(qn[b, h], kn[page, off, kvh])) * scale
-            w = np.exp(logits - logits.max())
-            w /= w.sum()
-            acc = np.zeros(D)
-            for t in range(L):
-                page, off = int(bt[b, t // P]), t % P
-                acc += w[t] * vn[page, off, kvh]
-            out[b, h] = acc
-    return out
+        for i in range(SQ):
+            n_vis = min(L, L - SQ + i + 1) if causal else L
+            if n_vis <= 0:
+                continue
+            for h in range(Hq):
+                kvh = h // G
+                logits = np.empty(n_vis)
+                for t in range(n_vis):
+                    page, off = int(bt[b, t // P]), t % P
+                    logits[t] = float(np.dot(qn[b, i, h], kn[page, off, kvh])) * scale
+                w = np.exp(logits - logits.max())
+                w /= w.sum()
+                acc = np.zeros(D)
+                for t in range(n_vis):
+                    page, off = int(bt[b, t // P]), t % P
+                    acc += w[t] * vn[page, off, kvh]
+                out[b, i, h] = acc
+    return out if qt.dim() == 4 else out[:, 0]
 
 
 def split_partials(q, k_cache, v_cache, block_table, seq_lens, tokens_per_split: int,

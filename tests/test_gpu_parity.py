@@ -377,3 +377,67 @@ def test_balanced_multi_block_length_scan(B, Hq, Hkv, D):
         out = _decode(inp, num_splits=ns)
         _check(inp, out, _sample(B, 24, seed=B), label=f"B={B} D={D} ns={ns}")
         assert read_device_status() == 0
+
+
+# ------------------------------------------------------------------------------------------
+# Multi-token queries (seqlen_q > 1, speculative-decode verification) and causal decode
+# ------------------------------------------------------------------------------------------
+
+MQ_LENS = [1, 3, 15, 16, 17, 100, 1000, 64, 2]
+
+
+def _mq_check(inp, out, causal, label):
+    ref = paged_decode_reference(inp.q.cpu(), inp.k_cache.cpu(), inp.v_cache.cpu(),
+                                 inp.block_table.cpu(), inp.seq_lens.cpu(), inp.scale,
+                                 causal=causal)
+    assert out.shape == inp.q.shape
+    assert_close_to_oracle(out, ref, label)
+    return ref
+
+
+@pytest.mark.parametrize("ns", [0, 3, -7])
+@pytest.mark.parametrize("Hq,Hkv,D,P", [(32, 8, 128, 16), (28, 4, 64, 64), (8, 8, 256, 16),
+                                        (32, 2, 128, 32)])
+@pytest.mark.parametrize("sq", [2, 4, 5, 8])
+@pytest.mark.parametrize("causal", [False, True])
+def test_multi_token_queries(causal, sq, Hq, Hkv, D, P, ns):
+    spec = W.custom_spec("mq", MQ_LENS, Hq, Hkv, D, P, seqlen_q=sq)
+    inp = W.make_inputs(spec, seed=sq * 7 + D, device=DEV)
+    out = _decode(inp, causal=causal, num_splits=ns)
+    ref = _mq_check(inp, out, causal, f"sq={sq} causal={causal} ns={ns}")
+    if causal:
+        # rows that see no key (L - sq + i + 1 <= 0) are exact zeros
+        for b, L in enumerate(MQ_LENS):
+            for i in range(sq):
+                if L - sq + i + 1 <= 0:
+                    assert not out[b, i].float().abs().any().item()
+                    assert not ref[b, i].abs().any().item()
+
+
+@pytest.mark.parametrize("ns", [1, 8, -200])
+def test_causal_long_sequence_across_splits(ns):
+    """Causal rows whose limits fall inside the last chunks, with the sequence cut into many
+    splits / pieces (split-grid combine and balanced merge tree carry the per-row masks)."""
+    spec = W.custom_spec("mq_long", [5000, 4093, 17], 32, 8, 128, 16, seqlen_q=6)
+    inp = W.make_inputs(spec, seed=11, device=DEV)
+    out = _decode(inp, causal=True, num_splits=ns)
+    _mq_check(inp, out, True, f"long causal ns={ns}")
+
+
+def test_multi_token_causal_via_run_kernel():
+    """The drop-in symbol with seqlen_q = 4 and causal = 1 (the reference fixes 1 and 0)."""
+    spec = W.custom_spec("mq_rk", [512, 1, 200, 480], 32, 4, 128, 16, max_pages=32,
+                         seqlen_q=4)
+    inp = W.make_inputs(spec, seed=3, device=DEV)
+    out = torch.zeros_like(inp.q)
+    run_kernel(inp.q, inp.k_cache, inp.v_cache, out, inp.seq_lens, inp.block_table,
+               4, 512, 4, 32, 4, 128, 16, 4 * 32, 1)
+    torch.cuda.synchronize()
+    _mq_check(inp, out, True, "run_kernel sq=4 causal")
+
+
+def test_single_token_causal_equals_non_causal():
+    inp = W.make_inputs(W.custom_spec("c1", MQ_LENS, 32, 8, 128, 16), seed=4, device=DEV)
+    a = _decode(inp, causal=False).clone()
+    b = _decode(inp, causal=True)
+    assert torch.equal(a, b)

@@ -68,16 +68,16 @@ PARTIAL_BASE = 256 + 4 * (4096 + 8192) * 4   # status word + fixed merge-counter
 
 
 def _decode(**over):
-    args = dict(q=FAKE, k=FAKE, v=FAKE, out=FAKE, lens=FAKE, table=FAKE, B=2, Hq=32, Hkv=8,
-                D=128, P=16, pages=64, max_pages=32, max_seq=0, scale=0.088, ns=2,
-                ws=FAKE, ws_bytes=1 << 30, phase=0, stream=None)
+    args = dict(q=FAKE, k=FAKE, v=FAKE, out=FAKE, lens=FAKE, table=FAKE, B=2, SQ=1, Hq=32,
+                Hkv=8, D=128, P=16, pages=64, max_pages=32, max_seq=0, causal=0, scale=0.088,
+                ns=2, ws=FAKE, ws_bytes=1 << 30, phase=0, stream=None)
     args.update(over)
     lib = _lib.load()
     return lib.mx_paged_gqa_decode(args["q"], args["k"], args["v"], args["out"], args["lens"],
-                                   args["table"], args["B"], args["Hq"], args["Hkv"], args["D"],
-                                   args["P"], args["pages"], args["max_pages"], args["max_seq"],
-                                   args["scale"], args["ns"], args["ws"], args["ws_bytes"],
-                                   args["phase"], args["stream"])
+                                   args["table"], args["B"], args["SQ"], args["Hq"], args["Hkv"],
+                                   args["D"], args["P"], args["pages"], args["max_pages"],
+                                   args["max_seq"], args["causal"], args["scale"], args["ns"],
+                                   args["ws"], args["ws_bytes"], args["phase"], args["stream"])
 
 
 @pytest.mark.parametrize("field", ["q", "k", "v", "out", "lens", "table"])
@@ -100,6 +100,10 @@ def test_null_pointers_are_rejected(field):
     (dict(P=48), _lib.MX_STATUS_UNSUPPORTED),
     (dict(Hq=64, Hkv=2), _lib.MX_STATUS_UNSUPPORTED),     # group 32 > 16
     (dict(B=70000), _lib.MX_STATUS_UNSUPPORTED),
+    (dict(SQ=0), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(B=300, SQ=300), _lib.MX_STATUS_UNSUPPORTED),    # combine grid: batch * seqlen_q
+    (dict(causal=2), _lib.MX_STATUS_INVALID_ARGUMENT),
+    (dict(ns=-3, B=512, Hkv=8, Hq=128, SQ=4), _lib.MX_STATUS_UNSUPPORTED),  # 16384 units
     (dict(phase=3), _lib.MX_STATUS_INVALID_ARGUMENT),
     (dict(scale=float("nan")), _lib.MX_STATUS_INVALID_ARGUMENT),
     (dict(scale=float("inf")), _lib.MX_STATUS_INVALID_ARGUMENT),
@@ -121,8 +125,8 @@ def _run_kernel(**over):
 
 
 @pytest.mark.parametrize("over,status", [
-    (dict(seqlen_q=2), _lib.MX_STATUS_UNSUPPORTED),
-    (dict(causal=1), _lib.MX_STATUS_UNSUPPORTED),
+    (dict(seqlen_q=0), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(causal=2), _lib.MX_STATUS_INVALID_ARGUMENT),
     (dict(nb=130), _lib.MX_STATUS_INVALID_SHAPE),
     (dict(nb=2), _lib.MX_STATUS_INVALID_SHAPE),
     (dict(seqlen_k=0), _lib.MX_STATUS_INVALID_SHAPE),
@@ -217,3 +221,33 @@ def test_policy_on_the_north_star_configs():
         sched, n = expect[name]
         assert p["schedule"] == sched, name
         assert (p["workgroups"] if sched == "balanced" else p["splits"]) == n, name
+
+
+@pytest.mark.parametrize("SQ,Hq,Hkv,tiles", [
+    (1, 32, 8, 1), (4, 32, 8, 1), (5, 32, 8, 2), (8, 64, 8, 4), (16, 8, 8, 1), (17, 8, 8, 2),
+    (3, 28, 4, 2),
+])
+def test_multi_token_row_tiles(SQ, Hq, Hkv, tiles):
+    """seqlen_q * group query rows per KV head run in tiles of 16: the split grid launches
+    Hkv * tiles workgroups per (sequence, split), its partial rows are per (token, head), and
+    the balanced schedule counts units per (sequence, KV head, tile)."""
+    G = Hq // Hkv
+    assert tiles == math.ceil(SQ * G / 16)
+    p = plan(2, Hq, Hkv, 128, 16, 64, 0, 3, num_cus=256, seqlen_q=SQ)
+    assert p["schedule"] == "split_grid" and p["splits"] == 3
+    assert p["workgroups"] == 2 * Hkv * tiles * 3
+    rows = 2 * SQ * Hq * 3
+    assert p["workspace_bytes"] == PARTIAL_BASE + math.ceil(rows * 4 / 256) * 256 + rows * 128 * 4
+    b = plan(64, Hq, Hkv, 128, 16, 64, 0, -100, num_cus=256, seqlen_q=SQ)
+    slots = 100 + 64 * Hkv * tiles
+    tr = min(16, SQ * G)
+    assert b["schedule"] == "balanced"
+    assert b["workspace_bytes"] == (PARTIAL_BASE + math.ceil(slots * tr * 4 / 256) * 256
+                                    + slots * tr * 128 * 4)
+
+
+@pytest.mark.skipif(gpu_available(), reason="would launch on the fake pointers")
+def test_run_kernel_accepts_multi_token_causal_arguments():
+    """seqlen_q > 1 and causal = 1 pass validation: without a device the call gets as far as
+    the device query."""
+    assert _run_kernel(seqlen_q=4, causal=1) == _lib.MX_STATUS_HIP_ERROR

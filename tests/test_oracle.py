@@ -252,3 +252,86 @@ def test_oracle_matches_golden(name):
     inp, expected = load_golden(name)
     out = _ref(inp)
     assert (out - expected).abs().max().item() < 2e-6
+
+
+# ---------------------------------------------------------------------------------------
+# Multi-token queries (seqlen_q > 1) and the end-aligned causal mask
+# ---------------------------------------------------------------------------------------
+
+def _mq_case(lens, Hq, Hkv, D, P, sq, seed=0):
+    spec = W.custom_spec("mq", lens, Hq, Hkv, D, P, seqlen_q=sq)
+    return W.make_inputs(spec, seed=seed)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("lens,Hq,Hkv,D,P,sq", [
+    ([1, 5, 17, 40], 8, 2, 64, 16, 3),      # L < seqlen_q: early causal rows see no key
+    ([33, 2], 28, 4, 32, 16, 2),             # group 7
+    ([70], 16, 16, 64, 32, 5),               # group 1
+])
+def test_multi_token_fp32_oracle_matches_fp64_brute_force(lens, Hq, Hkv, D, P, sq, causal):
+    inp = _mq_case(lens, Hq, Hkv, D, P, sq, seed=sq + D)
+    got = _ref(inp, causal=causal).double().numpy()
+    exp = paged_decode_fp64(inp.q, inp.k_cache, inp.v_cache, inp.block_table, inp.seq_lens,
+                            inp.scale, causal=causal)
+    assert got.shape == tuple(inp.q.shape)
+    assert np.abs(got - exp).max() < 2e-6
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_multi_token_rows_are_single_token_decodes(causal):
+    """Query token i of seqlen_q is a one-token decode of q[:, i] over the first L keys, or
+    over the first L - seqlen_q + i + 1 keys with the end-aligned causal mask (zeros when that
+    is <= 0), checked against the single-token fp64 brute force pinned above."""
+    sq = 4
+    inp = _mq_case([2, 9, 16, 47], 16, 4, 64, 16, sq, seed=5)
+    out = _ref(inp, causal=causal).double().numpy()
+    for i in range(sq):
+        lens = inp.seq_lens - (sq - 1 - i) if causal else inp.seq_lens
+        single = paged_decode_fp64(inp.q[:, i], inp.k_cache, inp.v_cache, inp.block_table,
+                                   lens, inp.scale)
+        assert np.abs(out[:, i] - single).max() < 2e-6, i
+
+
+def test_causal_square_case_matches_torch_sdpa_is_causal():
+    """With seqlen_q == L the end-aligned mask is the ordinary lower triangle, which torch's
+    scaled_dot_product_attention(is_causal=True) computes itself; the last query row of any
+    causal call sees every key (equal to the non-causal row)."""
+    torch.manual_seed(3)
+    Hq, Hkv, D, P, L = 8, 2, 64, 16, 37
+    npg = math.ceil(L / P)
+    q = torch.randn(1, L, Hq, D).to(torch.bfloat16)
+    k = torch.randn(npg, P, Hkv, D).to(torch.bfloat16)
+    v = torch.randn(npg, P, Hkv, D).to(torch.bfloat16)
+    table = torch.arange(npg, dtype=torch.int32).view(1, npg)
+    lens = torch.tensor([L], dtype=torch.int32)
+    out = paged_decode_reference(q, k, v, table, lens, 1 / math.sqrt(D), causal=True)
+    kk = k.view(npg * P, Hkv, D)[:L].double().permute(1, 0, 2).repeat_interleave(Hq // Hkv, 0)
+    vv = v.view(npg * P, Hkv, D)[:L].double().permute(1, 0, 2).repeat_interleave(Hq // Hkv, 0)
+    exp = F.scaled_dot_product_attention(q[0].double().permute(1, 0, 2), kk, vv,
+                                         is_causal=True)          # [Hq, L, D]
+    assert torch.allclose(out[0].double(), exp.permute(1, 0, 2), atol=1e-5)
+    full = paged_decode_reference(q, k, v, table, lens, 1 / math.sqrt(D), causal=False)
+    assert torch.equal(out[:, -1], full[:, -1])
+
+
+def _causal_mutant(kind, inp):
+    """Copies of the causal rule with plausible mistakes: the top-left aligned mask (query i
+    sees keys t <= i) and an end-aligned mask off by one (t < L - seqlen_q + i)."""
+    B, sq, Hq, D = inp.q.shape
+    out = torch.zeros(B, sq, Hq, D, dtype=torch.float64)
+    for i in range(sq):
+        if kind == "top_left":
+            lens = torch.clamp(inp.seq_lens, max=i + 1)
+        else:
+            lens = inp.seq_lens - (sq - i)
+        out[:, i] = torch.from_numpy(paged_decode_fp64(inp.q[:, i], inp.k_cache, inp.v_cache,
+                                                       inp.block_table, lens, inp.scale))
+    return out
+
+
+@pytest.mark.parametrize("kind", ["top_left", "off_by_one"])
+def test_planted_causal_mistakes_are_caught(kind):
+    inp = _mq_case([5, 30, 64], 8, 2, 32, 16, 4, seed=9)
+    exp = _ref(inp, causal=True).double()
+    assert (torch.as_tensor(_causal_mutant(kind, inp)) - exp).abs().max().item() > 1e-3
