@@ -19,6 +19,7 @@ after the second event).  Prints ONE JSON line:
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -75,11 +76,12 @@ def time_workload(inp: W.DecodeInputs, steps: int, warmup: int, num_splits: int 
     pools = [(inp.k_cache, inp.v_cache)] + [(inp.k_cache.clone(), inp.v_cache.clone())
                                             for _ in range(copies - 1)]
     plan = pkg.plan(spec.batch, spec.num_heads, spec.num_kv_heads, spec.head_dim,
-                    spec.page_size, spec.max_pages, 0, num_splits)
+                    spec.page_size, spec.max_pages, 0, num_splits, seqlen_q=spec.seqlen_q)
     ws = pkg.make_workspace(plan["workspace_bytes"], inp.device)
     out = torch.empty_like(inp.q)
     calls = [pkg.BoundDecode(inp.q, k, v, inp.block_table, inp.seq_lens, inp.scale, out=out,
-                             num_splits=num_splits, workspace=ws, stream=stream)
+                             causal=spec.causal, num_splits=num_splits, workspace=ws,
+                             stream=stream)
              for k, v in pools]
     split = plan["splits"] > 1
     main_phase = _lib.MX_PHASE_MAIN_ONLY if split else _lib.MX_PHASE_ALL
@@ -127,6 +129,55 @@ def time_workload(inp: W.DecodeInputs, steps: int, warmup: int, num_splits: int 
         "value_gbps": nbytes / (ms_per_step * 1e-3) / 1e9,
         "kernel_gbps": nbytes / (kern_mean * 1e-6) / 1e9,
     }
+
+
+def time_append(spec: W.DecodeSpec, steps: int, warmup: int, seed: int = 0) -> dict:
+    """Time the paged K/V append of one new token per sequence of `spec` (the step before the
+    decode): bytes are the new rows read plus the page slots written."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    B, Hkv, D = spec.batch, spec.num_kv_heads, spec.head_dim
+    inp = W.make_inputs(spec, seed=seed, device="cuda")
+    lens = (inp.seq_lens - 1).clamp(min=0)   # append the last token of each sequence
+    kn = torch.randn(B, Hkv, D, generator=g, device="cuda").to(torch.bfloat16)
+    vn = torch.randn(B, Hkv, D, generator=g, device="cuda").to(torch.bfloat16)
+    ws = pkg.make_workspace(256, "cuda")
+    stream = torch.cuda.current_stream()
+    # validated once through the tensor API, then called with pre-built C arguments so the
+    # host-side Python wrapper does not pace the GPU
+    pkg.paged_kv_append(kn, vn, inp.k_cache, inp.v_cache, inp.block_table, lens, workspace=ws,
+                        stream=stream)
+    fn = _lib.load().mx_paged_kv_append
+    cargs = [ctypes.c_void_p(t.data_ptr()) for t in (kn, vn, inp.k_cache, inp.v_cache, lens,
+                                                     inp.block_table)]
+    cargs += [B, 1, Hkv, D, spec.page_size, inp.k_cache.shape[0], inp.block_table.shape[1],
+              ctypes.c_void_p(ws.data_ptr()), ctypes.c_void_p(stream.cuda_stream)]
+
+    def call():
+        st = fn(*cargs)
+        if st != _lib.MX_STATUS_OK:
+            _lib.check(st)
+
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        call()
+    end.record(stream)
+    torch.cuda.synchronize()
+    if pkg.read_device_status(ws):
+        raise RuntimeError("device status flags raised during the append benchmark")
+    us = start.elapsed_time(end) * 1e3 / steps
+    nbytes = 2 * 2 * B * Hkv * D * 2   # K and V rows, read once and written once
+    del inp
+    torch.cuda.empty_cache()
+    return {"metric": "paged_kv_append_us_per_call", "value": round(us, 2), "unit": "us",
+            "higher_is_better": False, "steps": steps, "dtype": "bf16",
+            "config": {"workload": f"append_{spec.name}", "batch": B, "seqlen_new": 1,
+                       "num_kv_heads": Hkv, "head_dim": D, "page_size": spec.page_size},
+            "bytes_per_call": nbytes, "GBps": round(nbytes / us / 1e3, 2),
+            "note": "launch-bound: one token per sequence moves bytes_per_call"}
 
 
 def cpu_baseline(inp: W.DecodeInputs, budget_s: float) -> dict:
@@ -257,7 +308,7 @@ def main(argv=None) -> int:
         del src, dst
         torch.cuda.empty_cache()
     if args.all:
-        for name in W.NORTH_STAR:
+        for name in list(W.NORTH_STAR) + list(W.EXTRA):
             if name == spec.name:
                 continue
             extra = W.make_inputs(name, seed=args.seed, device="cuda")
@@ -268,6 +319,8 @@ def main(argv=None) -> int:
             print(json.dumps(result_line(a2, extra.spec, rr)), flush=True)
             del extra
             torch.cuda.empty_cache()
+        print(json.dumps(time_append(W.get_spec(W.BENCH_DEFAULT), 200, 20, args.seed)),
+              flush=True)
     print(json.dumps(line), flush=True)
     return 0
 

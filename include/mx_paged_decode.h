@@ -145,6 +145,31 @@ int64_t mx_paged_gqa_decode_workspace_size(int64_t batch, int64_t seqlen_q, int6
                                            int64_t page_size, int64_t max_pages_per_seq,
                                            int64_t max_seq_len, int64_t num_splits);
 
+/*
+ * Paged KV-cache append: writes seqlen_new new tokens per sequence into their page slots, the
+ * step that fills the layout the decode reads.  No counterpart in the reference, whose harness
+ * fills pages with torch.randn (bench_all.py:31-33); the semantics are those of the k / v
+ * arguments of flash_attn_with_kvcache, which the reference's harness passes as None
+ * (verify_real.py:40-41): token j of sequence b is stored at position
+ * pos = max(seq_lens[b], 0) + j, i.e. page block_table[b, pos / page_size], offset
+ * pos % page_size.
+ *   k_new, v_new   [batch, seqlen_new, num_kv_heads, head_dim] bf16, 16-byte aligned.
+ *   k_cache, v_cache, block_table, page_size, max_pages_per_seq: as for the decode.
+ *   seq_lens       lengths BEFORE the append; not modified (the caller adds seqlen_new).
+ *   num_pages      pool size (required, >= 1): a page id outside [0, num_pages) is flagged
+ *                  (MX_DEVICE_BAD_PAGE_ID) and its token skipped; a position past the table
+ *                  row is flagged (MX_DEVICE_SEQ_TOO_LONG) and skipped.  Nothing is written
+ *                  outside the pool.
+ *   workspace      any decode workspace (its status word receives the flags), NULL = the
+ *                  library's.
+ * Asynchronous on `stream`; head_dim must be a multiple of 8.  Returns MX_STATUS_*.
+ */
+int mx_paged_kv_append(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                       const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
+                       int64_t seqlen_new, int64_t num_kv_heads, int64_t head_dim,
+                       int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
+                       void* workspace, void* stream);
+
 /* Copies the sticky device status word (MX_DEVICE_* bits) of a workspace (NULL = the library's
  * workspace of the current device) to *flags_out after synchronising the stream; clears it
  * when reset != 0.  Not part of the reference (which validates nothing on the device). */

@@ -11,6 +11,7 @@ from .decode import (  # noqa: F401
     BoundDecode,
     make_workspace,
     paged_gqa_decode,
+    paged_kv_append,
     plan,
     read_device_status,
     run_kernel,
@@ -24,6 +25,7 @@ __all__ = [
     "load",
     "make_workspace",
     "paged_gqa_decode",
+    "paged_kv_append",
     "plan",
     "read_device_status",
     "run_kernel",

@@ -1103,6 +1103,45 @@ __global__ __launch_bounds__(64) void mx_paged_decode_combine(
 }
 
 // ------------------------------------------------------------------------------------------
+// Paged KV-cache append: the new tokens' K/V rows into their block-table slots
+// ------------------------------------------------------------------------------------------
+
+// One wave per (new token, K or V).  A token's Hkv * D values are contiguous both in the
+// new-token tensor [batch, seqlen_new, Hkv, D] and in its page slot [page, offset, Hkv, D], so
+// the copy is row_vec16 = Hkv * D / 8 16-byte vectors.  Token j of sequence b goes to position
+// pos = max(seq_lens[b], 0) + j: page block_table[b, pos / page_size], offset
+// pos % page_size.  A position past the table row or a page id outside [0, num_pages) is
+// flagged and skipped, so nothing is ever written outside the pool.
+__global__ __launch_bounds__(256) void mx_paged_kv_append_kernel(
+    const uint16_t* __restrict__ k_new, const uint16_t* __restrict__ v_new,
+    uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
+    const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ block_table, int batch,
+    int seqlen_new, int row_vec16, int page_size, int num_pages, int max_pages,
+    uint32_t* __restrict__ status) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
+  if (wave >= 2 * batch * seqlen_new) return;
+  const int tok = wave >> 1;  // neighbouring waves copy the K and V rows of one token
+  const bool is_v = (wave & 1) != 0;
+  const int b = tok / seqlen_new;
+  const int j = tok - b * seqlen_new;
+  const int pos = max(seq_lens[b], 0) + j;
+  if (pos >= max_pages * page_size) {
+    if (lane == 0 && !is_v) atomicOr(status, (uint32_t)MX_DEVICE_SEQ_TOO_LONG);
+    return;
+  }
+  const int pid = block_table[(int64_t)b * max_pages + pos / page_size];
+  if (pid < 0 || pid >= num_pages) {
+    if (lane == 0 && !is_v) atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
+    return;
+  }
+  const u32x4* src = reinterpret_cast<const u32x4*>(is_v ? v_new : k_new) + (int64_t)tok * row_vec16;
+  u32x4* dst = reinterpret_cast<u32x4*>(is_v ? v_cache : k_cache) +
+               ((int64_t)pid * page_size + pos % page_size) * row_vec16;
+  for (int i = lane; i < row_vec16; i += 64) dst[i] = src[i];
+}
+
+// ------------------------------------------------------------------------------------------
 // Host side: errors, planning, workspace, launch
 // ------------------------------------------------------------------------------------------
 
@@ -1558,6 +1597,49 @@ int mx_read_device_status(void* workspace, int32_t reset, void* stream, int32_t*
     }
   }
   *flags_out = (int32_t)word;
+  return ok();
+}
+
+int mx_paged_kv_append(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                       const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
+                       int64_t seqlen_new, int64_t num_kv_heads, int64_t head_dim,
+                       int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
+                       void* workspace, void* stream) {
+  if (!k_new || !v_new || !k_cache || !v_cache || !seq_lens || !block_table)
+    return fail(MX_STATUS_NULL_POINTER,
+                "k_new, v_new, k_cache, v_cache, seq_lens and block_table must be non-NULL");
+  for (const void* p : {k_new, v_new, static_cast<const void*>(k_cache),
+                        static_cast<const void*>(v_cache)})
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
+      return fail(MX_STATUS_INVALID_ARGUMENT, "K/V tensors must be 16-byte aligned");
+  if (batch < 1 || seqlen_new < 0 || num_kv_heads < 1 || head_dim < 1 || page_size < 1 ||
+      max_pages_per_seq < 1)
+    return fail(MX_STATUS_INVALID_SHAPE,
+                "batch, num_kv_heads, head_dim, page_size and max_pages_per_seq must be >= 1 "
+                "and seqlen_new >= 0");
+  if (num_pages < 1)
+    return fail(MX_STATUS_INVALID_SHAPE,
+                "num_pages (the pool size) must be >= 1: it bounds every write");
+  if (head_dim % 8 != 0) return fail(MX_STATUS_UNSUPPORTED, "head_dim must be a multiple of 8");
+  if (max_pages_per_seq > (int64_t)INT32_MAX / page_size || num_pages > INT32_MAX ||
+      num_kv_heads * head_dim > INT32_MAX / 8 ||
+      batch * seqlen_new > (int64_t)INT32_MAX / 2 - 4)
+    return fail(MX_STATUS_UNSUPPORTED, "sizes must fit 32-bit indices");
+  if (seqlen_new == 0) return ok();
+  if (workspace == nullptr) {
+    const int st = internal_workspace(kStatusBytes, &workspace);
+    if (st != MX_STATUS_OK) return st;
+  }
+  const int64_t waves = 2 * batch * seqlen_new;
+  hipLaunchKernelGGL(mx_paged_kv_append_kernel, dim3((unsigned)ceil_div(waves, 4)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(k_new),
+                     static_cast<const uint16_t*>(v_new), static_cast<uint16_t*>(k_cache),
+                     static_cast<uint16_t*>(v_cache), seq_lens, block_table, (int)batch,
+                     (int)seqlen_new, (int)(num_kv_heads * head_dim / 8), (int)page_size,
+                     (int)num_pages, (int)max_pages_per_seq, static_cast<uint32_t*>(workspace));
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail(MX_STATUS_HIP_ERROR, std::string("kernel launch failed: ") + hipGetErrorString(e));
   return ok();
 }
 

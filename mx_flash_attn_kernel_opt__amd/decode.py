@@ -189,6 +189,50 @@ def run_kernel(q, k_cache_paged, v_cache_paged, output, cache_seqlens, block_tab
     _lib.check(lib.mx_last_status())
 
 
+def paged_kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
+                    v_cache: torch.Tensor, block_table: torch.Tensor, seq_lens: torch.Tensor,
+                    *, workspace: torch.Tensor | None = None, stream=None) -> None:
+    """Write new tokens' K/V into their page slots (flash_attn_with_kvcache's k / v append).
+
+    k_new / v_new: [B, S, Hkv, D] (or [B, Hkv, D] for one token) bf16; token j of sequence b
+    goes to position max(seq_lens[b], 0) + j of that sequence's block-table row.  seq_lens are
+    the lengths before the append and are not modified.  Slots past the table row or with a
+    page id outside the pool are skipped and flagged (read_device_status).
+    """
+    _require(k_new.is_cuda, "k_new must be a device tensor")
+    dev = k_new.device
+    for name, t, dt in (("k_new", k_new, torch.bfloat16), ("v_new", v_new, torch.bfloat16),
+                        ("k_cache", k_cache, torch.bfloat16), ("v_cache", v_cache, torch.bfloat16),
+                        ("block_table", block_table, torch.int32),
+                        ("seq_lens", seq_lens, torch.int32)):
+        _require(t.device == dev, f"{name} must be on {dev}")
+        _require(t.dtype == dt, f"{name} must be {dt}, got {t.dtype}")
+        _require(t.is_contiguous(), f"{name} must be contiguous")
+    _require(k_new.shape == v_new.shape, "k_new and v_new must have the same shape")
+    _require(k_cache.dim() == 4 and k_cache.shape == v_cache.shape,
+             "k_cache and v_cache must both be [num_pages, page_size, Hkv, D]")
+    num_pages, P, Hkv, D = k_cache.shape
+    if k_new.dim() == 3:
+        B, S = k_new.shape[0], 1
+        _require(tuple(k_new.shape[1:]) == (Hkv, D), "k_new must be [B, Hkv, D] or [B, S, Hkv, D]")
+    else:
+        _require(k_new.dim() == 4 and tuple(k_new.shape[2:]) == (Hkv, D),
+                 "k_new must be [B, Hkv, D] or [B, S, Hkv, D]")
+        B, S = k_new.shape[0], k_new.shape[1]
+    _require(block_table.dim() == 2 and block_table.shape[0] == B,
+             "block_table must be [B, max_pages]")
+    _require(seq_lens.shape == (B,), "seq_lens must be [B]")
+    ws = None if workspace is None else workspace
+    if ws is not None:
+        _require(ws.is_cuda and ws.device == dev, "workspace must be on the same device")
+    with torch.cuda.device(dev):
+        st = _lib.load().mx_paged_kv_append(
+            _ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache), _ptr(seq_lens),
+            _ptr(block_table), B, S, Hkv, D, P, num_pages, block_table.shape[1], _ptr(ws),
+            _stream_handle(stream, dev))
+    _lib.check(st)
+
+
 def read_device_status(workspace: torch.Tensor | None = None, reset: bool = True,
                        stream=None, device=None) -> int:
     """Sticky MX_DEVICE_* bits raised by the kernels (synchronises the stream)."""

@@ -158,6 +158,18 @@ def _north_star_specs() -> dict[str, DecodeSpec]:
 NORTH_STAR = _north_star_specs()
 BENCH_DEFAULT = "llama3_8b"   # the metric's quoted workload
 
+# Measurement workloads beyond the north-star table: multi-token causal queries (speculative
+# decode verification) on the Llama-3-8B decode shape.  4 draft tokens x group 4 fill one
+# 16-row tile (same K/V traffic as the decode step); 8 tokens need two tiles.
+EXTRA = {
+    "specdec4_llama3_8b": DecodeSpec(
+        "specdec4_llama3_8b", 64, 32, 8, 128, 16, 256, "fixed", (4096,), seqlen_q=4,
+        causal=True, description="B=64 Hq=32 Hkv=8 D=128 P=16 L=4096, 4 causal query tokens"),
+    "specdec8_llama3_8b": DecodeSpec(
+        "specdec8_llama3_8b", 64, 32, 8, 128, 16, 256, "fixed", (4096,), seqlen_q=8,
+        causal=True, description="B=64 Hq=32 Hkv=8 D=128 P=16 L=4096, 8 causal query tokens"),
+}
+
 # The reference's case table: case -> (batch, seqlen_k capacity, num_heads_k)
 # (bench_all.py:58-63; warmup/iters of bench_all.py:64).
 C500_CASES = {
@@ -179,6 +191,8 @@ def c500_spec(case: int, table: str = "arange") -> DecodeSpec:
 def get_spec(name: str) -> DecodeSpec:
     if name in NORTH_STAR:
         return NORTH_STAR[name]
+    if name in EXTRA:
+        return EXTRA[name]
     if name.startswith("c500_case"):
         return c500_spec(int(name[len("c500_case"):]))
     raise KeyError(f"unknown workload {name!r}; known: {sorted(NORTH_STAR)} and c500_case1..14")

@@ -17,6 +17,10 @@ Pinning (what each function is checked against, in tests/test_oracle.py):
                           the split-KV + log-sum-exp merge (optimized_c500_flash_attn.cu:537-551,
                           666-728); pinned by equality with the unsplit oracle for every split
                           size.
+  paged_kv_append_reference
+                          the paged K/V append (flash_attn_with_kvcache's k / v); pinned by
+                          the round trip through the decode oracle against plain attention
+                          over the concatenated keys, computed by torch's SDPA.
 No reference-held fixtures exist for this path (the reference checks live against the absent
 third-party flash_attn_with_kvcache, verify_real.py:40-41), so parity with that library is
 unpinned; the task.md:85-96 example is kept as a shape fixture under tests/golden/.
@@ -27,5 +31,6 @@ from .paged_attention import (  # noqa: F401
     kv_bytes,
     paged_decode_fp64,
     paged_decode_reference,
+    paged_kv_append_reference,
     split_partials,
 )

@@ -181,3 +181,34 @@ def combine_partials(o: np.ndarray, lse: np.ndarray, nsv) -> np.ndarray:
         w = np.exp(lse[b, :, :n] - m)                              # [Hq, n]
         out[b] = (w[:, :, None] * o[b, :, :n]).sum(1) / w.sum(-1, keepdims=True)
     return out
+
+
+def paged_kv_append_reference(k_new, v_new, k_cache, v_cache, block_table, seq_lens):
+    """Paged K/V append on CPU copies (flash_attn_with_kvcache's k / v arguments; the reference's
+    harness passes them as None, verify_real.py:40-41): token j of sequence b is stored at
+    position pos = max(L_b, 0) + j, page block_table[b, pos // P], offset pos % P
+    (task.md:94, 146).  Slots past the table row or with a page id outside the pool are
+    skipped.  Returns (k_cache, v_cache, flags) with flags a set of {"seq_too_long",
+    "bad_page"}."""
+    k_out, v_out = k_cache.clone(), v_cache.clone()
+    kn = k_new if k_new.dim() == 4 else k_new.unsqueeze(1)
+    vn = v_new if v_new.dim() == 4 else v_new.unsqueeze(1)
+    B, S = kn.shape[0], kn.shape[1]
+    num_pages, P = k_cache.shape[0], k_cache.shape[1]
+    width = block_table.shape[1]
+    lens = torch.as_tensor(seq_lens).cpu()
+    flags = set()
+    for b in range(B):
+        for j in range(S):
+            pos = max(int(lens[b]), 0) + j
+            if pos >= width * P:
+                flags.add("seq_too_long")
+                continue
+            pid = int(block_table[b, pos // P])
+            if not 0 <= pid < num_pages:
+                flags.add("bad_page")
+                continue
+            k_out[pid, pos % P] = kn[b, j]
+            v_out[pid, pos % P] = vn[b, j]
+    return k_out, v_out, flags
+

@@ -251,3 +251,35 @@ def test_run_kernel_accepts_multi_token_causal_arguments():
     """seqlen_q > 1 and causal = 1 pass validation: without a device the call gets as far as
     the device query."""
     assert _run_kernel(seqlen_q=4, causal=1) == _lib.MX_STATUS_HIP_ERROR
+
+
+# ------------------------------------------------------------------------------------------
+# Paged K/V append: validation (no HIP call is reached on these paths)
+# ------------------------------------------------------------------------------------------
+
+def _append(**over):
+    a = dict(kn=FAKE, vn=FAKE, k=FAKE, v=FAKE, lens=FAKE, table=FAKE, B=4, S=1, Hkv=8, D=128,
+             P=16, pages=64, max_pages=16, ws=None, stream=None)
+    a.update(over)
+    return _lib.load().mx_paged_kv_append(a["kn"], a["vn"], a["k"], a["v"], a["lens"],
+                                          a["table"], a["B"], a["S"], a["Hkv"], a["D"], a["P"],
+                                          a["pages"], a["max_pages"], a["ws"], a["stream"])
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(kn=None), _lib.MX_STATUS_NULL_POINTER),
+    (dict(table=None), _lib.MX_STATUS_NULL_POINTER),
+    (dict(v=ctypes.c_void_p(0x1008)), _lib.MX_STATUS_INVALID_ARGUMENT),   # not 16-byte aligned
+    (dict(pages=0), _lib.MX_STATUS_INVALID_SHAPE),                        # pool size required
+    (dict(B=0), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(S=-1), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(D=100), _lib.MX_STATUS_UNSUPPORTED),
+    (dict(max_pages=1 << 28, P=16), _lib.MX_STATUS_UNSUPPORTED),
+])
+def test_append_rejects_invalid_arguments(over, status):
+    assert _append(**over) == status
+    assert _lib.load().mx_last_error()
+
+
+def test_append_of_zero_tokens_is_a_no_op():
+    assert _append(S=0) == _lib.MX_STATUS_OK

@@ -335,3 +335,86 @@ def test_planted_causal_mistakes_are_caught(kind):
     inp = _mq_case([5, 30, 64], 8, 2, 32, 16, 4, seed=9)
     exp = _ref(inp, causal=True).double()
     assert (torch.as_tensor(_causal_mutant(kind, inp)) - exp).abs().max().item() > 1e-3
+
+
+# ---------------------------------------------------------------------------------------
+# Paged K/V append (the producer of the page layout)
+# ---------------------------------------------------------------------------------------
+
+def _append_case(lens, S, Hkv=4, D=32, P=16, width=6, seed=0):
+    from oracle import paged_kv_append_reference
+    g = torch.Generator().manual_seed(seed)
+    B = len(lens)
+    pool = B * width + 3
+    k = torch.randn(pool, P, Hkv, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(pool, P, Hkv, D, generator=g).to(torch.bfloat16)
+    table = torch.randperm(pool, generator=g)[: B * width].to(torch.int32).view(B, width)
+    kn = torch.randn(B, S, Hkv, D, generator=g).to(torch.bfloat16)
+    vn = torch.randn(B, S, Hkv, D, generator=g).to(torch.bfloat16)
+    lens_t = torch.tensor(lens, dtype=torch.int32)
+    k2, v2, flags = paged_kv_append_reference(kn, vn, k, v, table, lens_t)
+    return k, v, table, kn, vn, lens_t, k2, v2, flags
+
+
+def test_append_then_decode_is_attention_over_the_concatenated_keys():
+    """Round trip: after appending S tokens, decoding L + S tokens equals plain attention
+    (torch SDPA) over [the L old rows; the S new rows], gathered independently."""
+    lens = [0, 5, 15, 16, 31, 40]
+    S = 3
+    k, v, table, kn, vn, lens_t, k2, v2, flags = _append_case(lens, S)
+    assert not flags
+    Hq, Hkv, D, P = 8, 4, 32, 16
+    q = torch.randn(len(lens), Hq, D, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    out = paged_decode_reference(q, k2, v2, table, lens_t + S, 1 / math.sqrt(D))
+    for b, L in enumerate(lens):
+        old_k = torch.stack([k[int(table[b, t // P]), t % P] for t in range(L)]) if L else \
+            torch.zeros(0, Hkv, D, dtype=torch.bfloat16)
+        old_v = torch.stack([v[int(table[b, t // P]), t % P] for t in range(L)]) if L else \
+            torch.zeros(0, Hkv, D, dtype=torch.bfloat16)
+        kk = torch.cat([old_k, kn[b]]).double().permute(1, 0, 2).repeat_interleave(Hq // Hkv, 0)
+        vv = torch.cat([old_v, vn[b]]).double().permute(1, 0, 2).repeat_interleave(Hq // Hkv, 0)
+        exp = F.scaled_dot_product_attention(q[b].double()[:, None], kk, vv)[:, 0]
+        assert torch.allclose(out[b].double(), exp, atol=1e-5), b
+
+
+def test_append_touches_only_the_new_slots():
+    lens = [7, 0, 30]
+    k, v, table, kn, vn, lens_t, k2, v2, flags = _append_case(lens, 4, seed=2)
+    changed = (k2 != k).flatten(2).any(-1) | (v2 != v).flatten(2).any(-1)   # [pool, P]
+    expect = torch.zeros_like(changed)
+    for b, L in enumerate(lens):
+        for j in range(4):
+            pos = L + j
+            expect[int(table[b, pos // 16]), pos % 16] = True
+    assert torch.equal(changed, expect)
+
+
+def test_append_flags_overflow_and_bad_pages():
+    from oracle import paged_kv_append_reference
+    k, v, table, kn, vn, lens_t, _, _, _ = _append_case([94, 10], 3, seed=4)   # row: 96 slots
+    table = table.clone()
+    table[1, 0] = 10_000
+    k2, v2, flags = paged_kv_append_reference(kn, vn, k, v, table, lens_t)
+    assert flags == {"seq_too_long", "bad_page"}
+    assert torch.equal(k2[int(table[0, 5]), 14:], kn[0, :2])   # positions 94, 95 written
+
+
+@pytest.mark.parametrize("kind", ["off_by_one", "page_offset_swapped"])
+def test_planted_append_mistakes_are_caught(kind):
+    """A mutant append (position L + j - 1, or page/offset computed as pos % width, pos // width)
+    fails the round-trip decode check."""
+    lens = [5, 20, 33]
+    S, P, width = 2, 16, 6
+    k, v, table, kn, vn, lens_t, k2, v2, _ = _append_case(lens, S, seed=6)
+    km, vm = k.clone(), v.clone()
+    for b, L in enumerate(lens):
+        for j in range(S):
+            pos = L + j - (1 if kind == "off_by_one" else 0)
+            page, off = ((int(table[b, pos // P]), pos % P) if kind == "off_by_one"
+                         else (int(table[b, pos % width]), min(pos // width, P - 1)))
+            km[page, off] = kn[b, j]
+            vm[page, off] = vn[b, j]
+    q = torch.randn(3, 8, 32, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    good = paged_decode_reference(q, k2, v2, table, lens_t + S)
+    bad = paged_decode_reference(q, km, vm, table, lens_t + S)
+    assert (good - bad).abs().max().item() > 1e-3
