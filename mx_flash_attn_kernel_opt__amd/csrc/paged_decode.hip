@@ -294,47 +294,56 @@ __device__ __forceinline__ void reset_state(SoftmaxState<D>& st) {
   st.l = 0.f;
 }
 
-// One chunk of the online softmax.  kMasked: only the first `nvalid` tokens of the chunk are
-// real (their V rows are kept, the others are replaced by zeros, so NaN or Inf in unused page
-// slots cannot reach the accumulators), and this lane's query row sees only the first
-// `row_valid` (<= nvalid) tokens: the causal limit of multi-token queries.  Scores of tokens a
-// row does not see become -inf.
-template <int D, bool kMasked>
-__device__ __forceinline__ void process_chunk(SoftmaxState<D>& st, const Chunk<D>& c,
-                                              const bf16x8 (&qop)[D / 32], float scale_log2,
-                                              int g4, int nvalid, int row_valid, char* klds,
-                                              int lane) {
-  // S^T[token][head] = K . Q^T  (16 tokens x 16 head slots, contraction over D)
+// One chunk of the online softmax for KT tiles of 16 query rows (the K and V operands are
+// shared by the tiles).  kMasked: only the first `nvalid` tokens of the chunk are real (their V
+// rows are kept, the others are replaced by zeros, so NaN or Inf in unused page slots cannot
+// reach the accumulators), and this lane's query row of tile t sees only the first
+// row_valid[t] (<= nvalid) tokens: the causal limit of multi-token queries.  Scores of tokens
+// a row does not see become -inf.
+template <int D, bool kMasked, int KT>
+__device__ __forceinline__ void process_chunk(SoftmaxState<D> (&st)[KT], const Chunk<D>& c,
+                                              const bf16x8 (&qop)[KT][D / 32], float scale_log2,
+                                              int g4, int nvalid, const int (&row_valid)[KT],
+                                              char* klds, int lane) {
+  // S^T[token][row] = K . Q^T  (16 tokens x 16 rows per tile, contraction over D)
   bf16x8 kop[D / 32];
   k_operands<D>(kop, c, klds, lane);
-  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  f32x4 s[KT];
 #pragma unroll
-  for (int i = 0; i < D / 32; ++i)
-    s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[i], qop[i], s, 0, 0, 0);
-  float x[4];
+  for (int t = 0; t < KT; ++t) {
+    s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    x[j] = s[j] * scale_log2;
-    if constexpr (kMasked) {
-      if (4 * g4 + j >= row_valid) x[j] = -INFINITY;
+    for (int i = 0; i < D / 32; ++i)
+      s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[i], qop[t][i], s[t], 0, 0, 0);
+  }
+  s16x4 pop[KT];
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    float x[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x[j] = s[t][j] * scale_log2;
+      if constexpr (kMasked) {
+        if (4 * g4 + j >= row_valid[t]) x[j] = -INFINITY;
+      }
     }
-  }
-  float cm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-  cm = group_max4(cm);
-  if (__builtin_amdgcn_ballot_w64(cm > st.m + kRescaleSlack)) {
-    const float mn = fmaxf(st.m, cm);
-    const float alpha = __builtin_amdgcn_exp2f(st.m - mn);
-    st.m = mn;
-    st.l *= alpha;
+    float cm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    cm = group_max4(cm);
+    if (__builtin_amdgcn_ballot_w64(cm > st[t].m + kRescaleSlack)) {
+      const float mn = fmaxf(st[t].m, cm);
+      const float alpha = __builtin_amdgcn_exp2f(st[t].m - mn);
+      st[t].m = mn;
+      st[t].l *= alpha;
 #pragma unroll
-    for (int i = 0; i < D / 16; ++i) st.o[i] *= alpha;
-  }
-  float p[4];
+      for (int i = 0; i < D / 16; ++i) st[t].o[i] *= alpha;
+    }
+    float p[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) p[j] = __builtin_amdgcn_exp2f(x[j] - st.m);
-  st.l += (p[0] + p[1]) + (p[2] + p[3]);
-  const u32x2 pw = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
-  const s16x4 pop = __builtin_bit_cast(s16x4, pw);
+    for (int j = 0; j < 4; ++j) p[j] = __builtin_amdgcn_exp2f(x[j] - st[t].m);
+    st[t].l += (p[0] + p[1]) + (p[2] + p[3]);
+    const u32x2 pw = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
+    pop[t] = __builtin_bit_cast(s16x4, pw);
+  }
 
   uint32_t v[4][D / 32];
 #pragma unroll
@@ -343,15 +352,17 @@ __device__ __forceinline__ void process_chunk(SoftmaxState<D>& st, const Chunk<D
 #pragma unroll
     for (int w = 0; w < D / 32; ++w) v[r][w] = keep ? c.v[r][w] : 0u;
   }
-  // O^T[d][head] += V^T . P^T  (tile i covers dims (D/16)*m + i, m = 0..15)
+  // O^T[d][row] += V^T . P^T  (tile i covers dims (D/16)*m + i, m = 0..15)
 #pragma unroll
   for (int i = 0; i < D / 16; ++i) {
     const int w = i >> 1;
     const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
     const u32x2 vw = {__builtin_amdgcn_perm(v[1][w], v[0][w], sel),
                       __builtin_amdgcn_perm(v[3][w], v[2][w], sel)};
-    st.o[i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, vw), pop,
-                                                        st.o[i], 0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < KT; ++t)
+      st[t].o[i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, vw),
+                                                             pop[t], st[t].o[i], 0, 0, 0);
   }
 }
 
@@ -439,17 +450,18 @@ __device__ __forceinline__ void load_q(bf16x8 (&qop)[D / 32], const uint16_t* q,
 }
 
 // Streams chunks c_lo + wv + k*NW (k >= 0, < c_hi) of one (sequence, KV head) through this
-// wave's register ring, accumulating into `st`.  The sequence holds `seq` tokens; chunks from
-// c_mask on (at least the last one) are processed with masks: tokens past the sequence end,
-// and with kCausal, for this lane's query row, the keys at or past row_lim.  Without kCausal
-// c_mask is the last chunk and row_lim is ignored.
-template <int D, int NBUF, int NW, bool kCausal>
-__device__ __forceinline__ void stream_chunks(SoftmaxState<D>& st, const bf16x8 (&qop)[D / 32],
+// wave's register ring, accumulating the KT row tiles into `st`.  The sequence holds `seq`
+// tokens; chunks from c_mask on (at least the last one) are processed with masks: tokens past
+// the sequence end, and with kCausal, for this lane's query row of tile t, the keys at or past
+// row_lim[t].  Without kCausal c_mask is the last chunk and row_lim is ignored.
+template <int D, int NBUF, int NW, bool kCausal, int KT>
+__device__ __forceinline__ void stream_chunks(SoftmaxState<D> (&st)[KT],
+                                              const bf16x8 (&qop)[KT][D / 32],
                                               const uint16_t* __restrict__ kc,
                                               const uint16_t* __restrict__ vc,
                                               const int32_t* __restrict__ bt_row, int kv,
                                               int c_lo, int c_hi, int seq, int c_mask,
-                                              int row_lim, int wv, char* klds,
+                                              const int (&row_lim)[KT], int wv, char* klds,
                                               const MainShape& sh, bool& bad_page) {
   constexpr int VW = D / 16;
   const int lane = threadIdx.x & 63;
@@ -479,9 +491,14 @@ __device__ __forceinline__ void stream_chunks(SoftmaxState<D>& st, const bf16x8 
   auto masked = [&](Chunk<D>& cb, int k) {
     const int t0 = gc(k) * kChunk;
     const int nvalid = min(kChunk, seq - t0);
-    const int row_valid = kCausal ? min(nvalid, row_lim - t0) : nvalid;
-    process_chunk<D, true>(st, cb, qop, sl2, g4, nvalid, row_valid, klds, lane);
+    int row_valid[KT];
+#pragma unroll
+    for (int t = 0; t < KT; ++t) row_valid[t] = kCausal ? min(nvalid, row_lim[t] - t0) : nvalid;
+    process_chunk<D, true, KT>(st, cb, qop, sl2, g4, nvalid, row_valid, klds, lane);
   };
+  int all_valid[KT];
+#pragma unroll
+  for (int t = 0; t < KT; ++t) all_valid[t] = kChunk;
 
   Chunk<D> buf[NBUF];
   auto load = [&](Chunk<D>& dst, int64_t base) { load_chunk<D>(dst, kc + base, vc + base, lo); };
@@ -501,7 +518,7 @@ __device__ __forceinline__ void stream_chunks(SoftmaxState<D>& st, const bf16x8 
       for (int i = 0; i < NBUF; ++i) nb[i] = chunk_base(gc(k + NBUF + i));
 #pragma unroll
       for (int i = 0; i < NBUF; ++i) {
-        process_chunk<D, false>(st, buf[i], qop, sl2, g4, kChunk, kChunk, klds, lane);
+        process_chunk<D, false, KT>(st, buf[i], qop, sl2, g4, kChunk, all_valid, klds, lane);
         load(buf[i], nb[i]);
       }
       k += NBUF;
@@ -545,63 +562,71 @@ __device__ __forceinline__ void stream_chunks(SoftmaxState<D>& st, const bf16x8 
 }
 
 // Workgroup LDS: the per-wave K transpose tiles while streaming, then (after a barrier) the
-// per-wave softmax states for the merge.  Rows of s_o are padded by 4 floats so the 16 head
-// rows written by one store instruction fall in different banks.
-template <int D, int NW>
+// per-wave softmax states of the 16*KT rows for the merge.  Rows of s_o are padded by 4 floats
+// so the 16 rows written by one store instruction fall in different banks.
+template <int D, int NW, int KT>
 struct GroupLds {
+  static constexpr int kRows = 16 * KT;
   static constexpr int kRow = D + 4;
   static constexpr int kKTile = k_via_lds<D>() ? 16 * 2 * D : 16;
-  static constexpr int kMergeBytes = NW * 16 * kRow * 4 + 2 * NW * 16 * 4;
+  static constexpr int kMergeBytes = NW * kRows * kRow * 4 + 2 * NW * kRows * 4;
   static constexpr int kBytes = (NW * kKTile > kMergeBytes) ? NW * kKTile : kMergeBytes;
   __device__ __forceinline__ static char* ktile(char* base, int wv) { return base + wv * kKTile; }
   __device__ __forceinline__ static float* o(char* base) { return reinterpret_cast<float*>(base); }
-  __device__ __forceinline__ static float* m(char* base) { return o(base) + NW * 16 * kRow; }
-  __device__ __forceinline__ static float* l(char* base) { return m(base) + NW * 16; }
+  __device__ __forceinline__ static float* m(char* base) { return o(base) + NW * kRows * kRow; }
+  __device__ __forceinline__ static float* l(char* base) { return m(base) + NW * kRows; }
 };
 
 // Writes every wave's state to LDS (after a barrier that ends the K-tile use of the same
 // bytes) and synchronises, so merged_head() can combine them.
-template <int D, int NW>
-__device__ __forceinline__ void publish_wave_state(char* lds, const SoftmaxState<D>& st, int wv) {
-  using L = GroupLds<D, NW>;
+template <int D, int NW, int KT>
+__device__ __forceinline__ void publish_wave_state(char* lds, const SoftmaxState<D> (&st)[KT],
+                                                   int wv) {
+  using L = GroupLds<D, NW, KT>;
   constexpr int VW = D / 16;
   const int lane = threadIdx.x & 63;
   const int h = lane & 15;
   const int g4 = lane >> 4;
-  const float l_w = group_sum4(st.l);
+  float l_w[KT];
+#pragma unroll
+  for (int t = 0; t < KT; ++t) l_w[t] = group_sum4(st[t].l);
   __syncthreads();
-  float* dst = L::o(lds) + (wv * 16 + h) * L::kRow + (D / 4) * g4;
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int t = 0; t < KT; ++t) {
+    const int row = wv * L::kRows + t * 16 + h;
+    float* dst = L::o(lds) + row * L::kRow + (D / 4) * g4;
 #pragma unroll
-    for (int i = 0; i < VW; i += 4)
-      *reinterpret_cast<f32x4*>(dst + VW * j + i) =
-          f32x4{st.o[i][j], st.o[i + 1][j], st.o[i + 2][j], st.o[i + 3][j]};
-  if (g4 == 0) {
-    L::m(lds)[wv * 16 + h] = st.m;
-    L::l(lds)[wv * 16 + h] = l_w;
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < VW; i += 4)
+        *reinterpret_cast<f32x4*>(dst + VW * j + i) =
+            f32x4{st[t].o[i][j], st[t].o[i + 1][j], st[t].o[i + 2][j], st[t].o[i + 3][j]};
+    if (g4 == 0) {
+      L::m(lds)[row] = st[t].m;
+      L::l(lds)[row] = l_w[t];
+    }
   }
   __syncthreads();
 }
 
-// Merged (normalised) dims d..d+3 of row slot hh and its log2-sum-exp; a row that saw no key
-// (l == 0: causal rows before their first key) is zeros with log2-sum-exp -inf.
-template <int D, int NW>
+// Merged (normalised) dims d..d+3 of row slot hh (< 16*KT) and its log2-sum-exp; a row that
+// saw no key (l == 0: causal rows before their first key) is zeros with log2-sum-exp -inf.
+template <int D, int NW, int KT>
 __device__ __forceinline__ f32x4 merged_head(const char* lds, int hh, int d, float& lse) {
-  using L = GroupLds<D, NW>;
+  using L = GroupLds<D, NW, KT>;
   const float* sm = L::m(const_cast<char*>(lds));
   const float* sl = L::l(const_cast<char*>(lds));
   float mx = sm[hh];
 #pragma unroll
-  for (int w = 1; w < NW; ++w) mx = fmaxf(mx, sm[w * 16 + hh]);
+  for (int w = 1; w < NW; ++w) mx = fmaxf(mx, sm[w * L::kRows + hh]);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   float lsum = 0.f;
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
-    const float a = __builtin_amdgcn_exp2f(sm[w * 16 + hh] - mx);
-    lsum += a * sl[w * 16 + hh];
+    const float a = __builtin_amdgcn_exp2f(sm[w * L::kRows + hh] - mx);
+    lsum += a * sl[w * L::kRows + hh];
     acc += a * *reinterpret_cast<const f32x4*>(L::o(const_cast<char*>(lds)) +
-                                              (w * 16 + hh) * L::kRow + d);
+                                              (w * L::kRows + hh) * L::kRow + d);
   }
   const bool seen = lsum > 0.f;
   lse = seen ? mx + log2f(lsum) : -INFINITY;
@@ -613,30 +638,46 @@ __device__ __forceinline__ void store_bf16x4(uint16_t* p, f32x4 v) {
   *reinterpret_cast<u32x2*>(p) = w;
 }
 
+// Row group g of a KV head: KT tiles of 16 rows, rows g*16*KT + t*16 + r16.  Loads the query
+// operands, clears the states and computes each lane's causal key limit per tile.
+template <int D, int KT>
+__device__ __forceinline__ void setup_row_group(bf16x8 (&qop)[KT][D / 32],
+                                                SoftmaxState<D> (&st)[KT], int (&row_lim)[KT],
+                                                const uint16_t* q, int b, int kv, int g, int seq,
+                                                const MainShape& sh, int lane) {
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    load_q<D>(qop[t], q, b, kv, g * KT + t, sh, lane);
+    reset_state<D>(st[t]);
+    row_lim[t] = row_key_limit((g * KT + t) * 16 + (lane & 15), seq, sh);
+  }
+}
+
 // ------------------------------------------------------------------------------------------
 // Split-grid kernel
 // ------------------------------------------------------------------------------------------
 
-// Grid (Hkv * row_tiles, batch, splits), NW waves per workgroup.  Consecutive workgroup ids,
-// which the dispatcher deals round-robin to the 8 XCDs, walk the KV heads (and row tiles) of
-// one sequence first, then the sequences, then the splits.  Every XCD therefore gets an even
-// share of the first split of every sequence (where ragged batches keep most of their work),
-// and the workgroups that read the same physical pages start together.
+// Grid (Hkv * row_tiles, batch, splits), NW waves per workgroup, row_tiles groups of KT 16-row
+// tiles per KV head.  Consecutive workgroup ids, which the dispatcher deals round-robin to the
+// 8 XCDs, walk the KV heads (and row groups) of one sequence first, then the sequences, then
+// the splits.  Every XCD therefore gets an even share of the first split of every sequence
+// (where ragged batches keep most of their work), and the workgroups that read the same
+// physical pages start together.
 //
-// The NW waves of a workgroup share one (KV head, row tile, sequence, split): wave wv streams
+// The NW waves of a workgroup share one (KV head, row group, sequence, split): wave wv streams
 // chunks c0+wv, c0+wv+NW, ... through its own register ring (so NW times more K/V bytes are in
 // flight per split, with no global partials), and the waves merge their (m, l, O) states
-// through LDS.
-template <int D, int NBUF, int NW, bool kCausal>
+// through LDS.  KT = 2 holds two tiles' states per wave, so one wave per SIMD (512 registers).
+template <int D, int NBUF, int NW, bool kCausal, int KT>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
-    D == 64 ? MX_WAVES_PER_EU_D64 : (D == 128 ? MX_WAVES_PER_EU_D128 : MX_WAVES_PER_EU_D256))))
+    KT == 2 ? 1 : (D == 64 ? MX_WAVES_PER_EU_D64 : (D == 128 ? MX_WAVES_PER_EU_D128 : MX_WAVES_PER_EU_D256)))))
 void mx_paged_decode_splitkv(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, uint16_t* __restrict__ out,
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ block_table,
     float* __restrict__ part_o, float* __restrict__ part_lse, uint32_t* __restrict__ status,
     const MainShape sh) {
-  using L = GroupLds<D, NW>;
+  using L = GroupLds<D, NW, KT>;
   __shared__ __attribute__((aligned(16))) char lds[L::kBytes];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -644,17 +685,18 @@ void mx_paged_decode_splitkv(
   // SGPRs and the page lookups remain scalar loads (off the vector-memory counter).
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kv = blockIdx.x / sh.row_tiles;
-  const int tile = blockIdx.x - kv * sh.row_tiles;
+  const int grp = blockIdx.x - kv * sh.row_tiles;  // row group: rows grp*16*KT ..
+  const int r0 = grp * 16 * KT;
   const int b = blockIdx.y;
   const int split = blockIdx.z;
-  const int nrows = min(16, sh.rows - tile * 16);  // query rows of this tile
+  const int nrows = min(16 * KT, sh.rows - r0);  // query rows of this group
 
   const int seq = clamped_len(seq_lens, b, sh, status, split == 0 && blockIdx.x == 0 && tid == 0);
   if (seq <= 0) {
     // Empty sequence: defined as a zero output.
     if (split == 0)
       for (int e = tid; e < nrows * (D / 4); e += 64 * NW)
-        store_bf16x4(out + (row_base(b, kv, sh) + row_offset(tile * 16 + e / (D / 4), sh)) * D +
+        store_bf16x4(out + (row_base(b, kv, sh) + row_offset(r0 + e / (D / 4), sh)) * D +
                          4 * (e % (D / 4)),
                      f32x4{0.f, 0.f, 0.f, 0.f});
     return;
@@ -664,27 +706,27 @@ void mx_paged_decode_splitkv(
   const int t1 = min(t0 + sh.tokens_per_split, seq);
   const bool single = seq <= sh.tokens_per_split;
   const int c_last = (seq - 1) / kChunk;
-  // First chunk any row of this tile must mask (causal), else the last chunk.
+  // First chunk any row of this group must mask (causal), else the last chunk.
   const int c_mask =
-      kCausal ? min(c_last, max(0, row_key_limit(tile * 16, seq, sh)) / kChunk) : c_last;
+      kCausal ? min(c_last, max(0, row_key_limit(r0, seq, sh)) / kChunk) : c_last;
 
-  bf16x8 qop[D / 32];
-  load_q<D>(qop, q, b, kv, tile, sh, lane);
-  SoftmaxState<D> st;
-  reset_state<D>(st);
+  bf16x8 qop[KT][D / 32];
+  SoftmaxState<D> st[KT];
+  int row_lim[KT];
+  setup_row_group<D, KT>(qop, st, row_lim, q, b, kv, grp, seq, sh, lane);
   bool bad_page = false;
-  stream_chunks<D, NBUF, NW, kCausal>(st, qop, kc, vc, block_table + (int64_t)b * sh.max_pages,
-                                      kv, t0 / kChunk, (t1 + kChunk - 1) / kChunk, seq, c_mask,
-                                      row_key_limit(tile * 16 + (lane & 15), seq, sh), wv,
-                                      L::ktile(lds, wv), sh, bad_page);
+  stream_chunks<D, NBUF, NW, kCausal, KT>(st, qop, kc, vc,
+                                          block_table + (int64_t)b * sh.max_pages, kv,
+                                          t0 / kChunk, (t1 + kChunk - 1) / kChunk, seq, c_mask,
+                                          row_lim, wv, L::ktile(lds, wv), sh, bad_page);
   if (bad_page && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
-  publish_wave_state<D, NW>(lds, st, wv);
+  publish_wave_state<D, NW, KT>(lds, st, wv);
   for (int e = tid; e < nrows * (D / 4); e += 64 * NW) {
     const int hh = e / (D / 4);
     const int d = 4 * (e - hh * (D / 4));
     float lse;
-    const f32x4 o = merged_head<D, NW>(lds, hh, d, lse);
-    const int64_t row = row_base(b, kv, sh) + row_offset(tile * 16 + hh, sh);
+    const f32x4 o = merged_head<D, NW, KT>(lds, hh, d, lse);
+    const int64_t row = row_base(b, kv, sh) + row_offset(r0 + hh, sh);
     if (single) {
       store_bf16x4(out + row * D + d, o);
     } else {
@@ -782,7 +824,7 @@ __device__ __forceinline__ int block_sum(int x, int* sred) {
 }
 
 // One launch of num_groups workgroups covers the whole batch whatever the length mix.  Every
-// (sequence b, KV head and row tile j) "unit" with n_b = ceil(L_b/16) > 0 chunks occupies n_b +
+// (sequence b, KV head and row group j) "unit" with n_b = ceil(L_b/16) > 0 chunks occupies n_b +
 // unit_overhead consecutive positions of one global line (units in (b, j) order; the
 // overhead charges the per-unit Q load and pipeline fill); workgroup w owns positions
 // [w*q, (w+1)*q) with q = ceil(total / num_groups), found from seq_lens on the device, so a
@@ -790,19 +832,19 @@ __device__ __forceinline__ int block_sum(int x, int* sred) {
 // entirely is written out as bf16; a unit cut into several pieces has each piece written as
 // a normalised partial (O/l, log2-sum-exp) to its own slot, and the last piece to finish
 // merges them through a fan-in-8 tree of per-unit counters, so the whole call is one launch.
-template <int D, int NBUF, int NW, bool kCausal>
+template <int D, int NBUF, int NW, bool kCausal, int KT>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
-    D == 64 ? MX_WAVES_PER_EU_D64 : (D == 128 ? MX_WAVES_PER_EU_D128 : MX_WAVES_PER_EU_D256))))
+    KT == 2 ? 1 : (D == 64 ? MX_WAVES_PER_EU_D64 : (D == 128 ? MX_WAVES_PER_EU_D128 : MX_WAVES_PER_EU_D256)))))
 void mx_paged_decode_balanced(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, uint16_t* __restrict__ out,
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ block_table,
     float* __restrict__ part_o, float* __restrict__ part_lse, uint32_t* __restrict__ counters,
     uint32_t* __restrict__ status, const MainShape sh) {
-  using L = GroupLds<D, NW>;
+  using L = GroupLds<D, NW, KT>;
   __shared__ __attribute__((aligned(16))) char lds[L::kBytes];
   __shared__ int s_int[NW + 4];
-  __shared__ float s_lse[16];
+  __shared__ float s_lse[16 * KT];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -895,7 +937,7 @@ void mx_paged_decode_balanced(
   int seq = clamped_len(seq_lens, b, sh, status, false);
   int n_b = (seq + kChunk - 1) / kChunk;
   int span = n_b + alpha;
-  int j = (x_begin - seq_start) / span;  // (KV head, row tile) of the unit
+  int j = (x_begin - seq_start) / span;  // (KV head, row group) of the unit
   int u0 = seq_start + j * span;  // first position of unit (b, j)
   const int per_level = kMaxSlots;  // counters of merge level l start at l * kMaxSlots
   bool bad_page = false;
@@ -908,33 +950,33 @@ void mx_paged_decode_balanced(
     if (ca < cb) {
       const int unit = b * UPS + j;
       const int kv = sh.row_tiles == 1 ? j : j / sh.row_tiles;
-      const int tile = j - kv * sh.row_tiles;
-      const int nrows = min(16, sh.rows - tile * 16);
+      const int grp = j - kv * sh.row_tiles;  // row group: rows grp*16*KT ..
+      const int r0 = grp * 16 * KT;
+      const int nrows = min(16 * KT, sh.rows - r0);
       const int64_t rbase = row_base(b, kv, sh);
       const int first_wg = cpos / qsz;
       const int npieces = (cpos + n_b - 1) / qsz - first_wg + 1;
       const int c_last = n_b - 1;
       const int c_mask =
-          kCausal ? min(c_last, max(0, row_key_limit(tile * 16, seq, sh)) / kChunk) : c_last;
+          kCausal ? min(c_last, max(0, row_key_limit(r0, seq, sh)) / kChunk) : c_last;
 
-      bf16x8 qop[D / 32];
-      load_q<D>(qop, q, b, kv, tile, sh, lane);
-      SoftmaxState<D> st;
-      reset_state<D>(st);
-      stream_chunks<D, NBUF, NW, kCausal>(st, qop, kc, vc,
-                                          block_table + (int64_t)b * sh.max_pages, kv, ca, cb,
-                                          seq, c_mask,
-                                          row_key_limit(tile * 16 + (lane & 15), seq, sh), wv,
-                                          L::ktile(lds, wv), sh, bad_page);
-      publish_wave_state<D, NW>(lds, st, wv);
+      bf16x8 qop[KT][D / 32];
+      SoftmaxState<D> st[KT];
+      int row_lim[KT];
+      setup_row_group<D, KT>(qop, st, row_lim, q, b, kv, grp, seq, sh, lane);
+      stream_chunks<D, NBUF, NW, kCausal, KT>(st, qop, kc, vc,
+                                              block_table + (int64_t)b * sh.max_pages, kv, ca,
+                                              cb, seq, c_mask, row_lim, wv, L::ktile(lds, wv),
+                                              sh, bad_page);
+      publish_wave_state<D, NW, KT>(lds, st, wv);
 
       if (npieces == 1) {
         for (int e = tid; e < nrows * (D / 4); e += 64 * NW) {
           const int hh = e / (D / 4);
           const int d = 4 * (e - hh * (D / 4));
           float lse;
-          store_bf16x4(out + (rbase + row_offset(tile * 16 + hh, sh)) * D + d,
-                       merged_head<D, NW>(lds, hh, d, lse));
+          store_bf16x4(out + (rbase + row_offset(r0 + hh, sh)) * D + d,
+                       merged_head<D, NW, KT>(lds, hh, d, lse));
         }
       } else {
         // Piece k of the unit goes to slot slot0 + k; level-l item j of the merge tree covers
@@ -948,7 +990,7 @@ void mx_paged_decode_balanced(
             const int hh = e / (D / 4);
             const int d = 4 * (e - hh * (D / 4));
             float lse;
-            store_partial4(po + hh * D + d, merged_head<D, NW>(lds, hh, d, lse));
+            store_partial4(po + hh * D + d, merged_head<D, NW, KT>(lds, hh, d, lse));
             if (d == 0) store_partial1(pl + hh, lse);
           }
         }
@@ -1001,7 +1043,7 @@ void mx_paged_decode_balanced(
             }
             acc *= seen ? 1.0f / wsum : 0.f;
             if (nnext == 1) {
-              store_bf16x4(out + (rbase + row_offset(tile * 16 + hh, sh)) * D + d, acc);
+              store_bf16x4(out + (rbase + row_offset(r0 + hh, sh)) * D + d, acc);
             } else {
               store_partial4(part_o + ((int64_t)gslot * TR + hh) * D + d, acc);
               if (d == 0) s_lse[hh] = seen ? mx + log2f(wsum) : -INFINITY;
@@ -1196,7 +1238,8 @@ struct Plan {
   int64_t groups = 0;             // balanced: workgroups of the launch
   int64_t slots = 0;              // balanced: partial slots (groups + units)
   int64_t rows = 1;               // query rows per KV head: seqlen_q * group
-  int64_t row_tiles = 1;          // ceil(rows / 16)
+  int64_t row_tiles = 1;          // row groups: ceil(rows / (16 * tiles_per_group))
+  int tiles_per_group = 1;        // 16-row tiles one pass over K/V serves (1, or 2 above 16 rows)
   int64_t cap_tokens = 0;
   int64_t counter_offset = 0;
   int64_t lse_offset = 0;
@@ -1251,12 +1294,16 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
     return fail(MX_STATUS_UNSUPPORTED, "batch * seqlen_q must be <= 65535");
   const int64_t group = num_heads / num_kv_heads;
   const int64_t rows = seqlen_q * group;
-  const int64_t row_tiles = ceil_div(rows, 16);
-  const int64_t tile_rows = std::min<int64_t>(rows, 16);
+  // Above 16 rows, one pass over a head's K/V serves two 16-row tiles (32 rows); at
+  // head_dim 256 two tiles' states do not fit the registers of a wave.
+  const int tiles_per_group = (rows > 16 && head_dim <= 128) ? 2 : 1;
+  const int64_t row_tiles = ceil_div(rows, 16 * tiles_per_group);
+  const int64_t tile_rows = std::min<int64_t>(rows, 16 * tiles_per_group);
   if (num_kv_heads * row_tiles > kMaxGridDim)
     return fail(MX_STATUS_UNSUPPORTED, "num_kv_heads * ceil(seqlen_q * group / 16) must be <= 65535");
   plan->rows = rows;
   plan->row_tiles = row_tiles;
+  plan->tiles_per_group = tiles_per_group;
   if (num_heads > kMaxGridDim) return fail(MX_STATUS_UNSUPPORTED, "num_heads must be <= 65535");
   if (max_pages > (int64_t)INT32_MAX / page_size)
     return fail(MX_STATUS_UNSUPPORTED, "max_pages_per_seq * page_size must fit in int32");
@@ -1382,7 +1429,7 @@ int internal_workspace(int64_t need, void** out) {
   return MX_STATUS_OK;
 }
 
-template <int D, bool kCausal>
+template <int D, bool kCausal, int KT>
 hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v, void* out,
                   const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
                   int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads, int64_t page_size,
@@ -1401,7 +1448,7 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   sh.causal = kCausal ? 1 : 0;
   sh.rows = (int)plan.rows;
   sh.row_tiles = (int)plan.row_tiles;
-  sh.tile_rows = (int)std::min<int64_t>(plan.rows, 16);
+  sh.tile_rows = (int)std::min<int64_t>(plan.rows, 16 * KT);
   sh.batch = (int)batch;
   sh.max_pages = (int)max_pages;
   sh.num_pages = (num_pages > 0 && num_pages <= INT32_MAX) ? (int)num_pages : 0;
@@ -1418,7 +1465,7 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   if (plan.schedule == MX_SCHEDULE_BALANCED) {
     // One launch does everything; MX_PHASE_COMBINE_ONLY has nothing left to do.
     if (phase == MX_PHASE_COMBINE_ONLY) return hipSuccess;
-    hipLaunchKernelGGL((mx_paged_decode_balanced<D, kNBUF, kNW, kCausal>),
+    hipLaunchKernelGGL((mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT>),
                        dim3((unsigned)plan.groups),
                        dim3(64 * kNW), 0, stream, static_cast<const uint16_t*>(q),
                        static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
@@ -1434,7 +1481,7 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   if (phase != MX_PHASE_COMBINE_ONLY) {
     const dim3 grid((unsigned)(num_kv_heads * plan.row_tiles), (unsigned)batch,
                     (unsigned)plan.splits);
-    hipLaunchKernelGGL((mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal>), grid, dim3(64 * kNW), 0,
+    hipLaunchKernelGGL((mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT>), grid, dim3(64 * kNW), 0,
                        stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                        static_cast<const uint16_t*>(v), static_cast<uint16_t*>(out), seq_lens,
                        block_table, part_o, part_lse, status, sh);
@@ -1526,19 +1573,22 @@ int mx_paged_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
   hipError_t e;
   // A causal mask changes nothing for a single query token (it sees every key).
   const bool masked = causal != 0 && seqlen_q > 1;
-#define MX_LAUNCH(DIM, CAUSAL)                                                                \
-  launch<DIM, CAUSAL>(plan, q, k_cache, v_cache, out, seq_lens, block_table, batch, seqlen_q,  \
+#define MX_LAUNCH(DIM, CAUSAL, KT)                                                            \
+  launch<DIM, CAUSAL, KT>(plan, q, k_cache, v_cache, out, seq_lens, block_table, batch, seqlen_q, \
                       num_heads, num_kv_heads, page_size, num_pages, max_pages_per_seq, scale, \
                       ws, phase, s)
+  const bool pair = plan.tiles_per_group == 2;
   switch (head_dim) {
     case 64:
-      e = masked ? MX_LAUNCH(64, true) : MX_LAUNCH(64, false);
+      e = pair ? (masked ? MX_LAUNCH(64, true, 2) : MX_LAUNCH(64, false, 2))
+               : (masked ? MX_LAUNCH(64, true, 1) : MX_LAUNCH(64, false, 1));
       break;
     case 128:
-      e = masked ? MX_LAUNCH(128, true) : MX_LAUNCH(128, false);
+      e = pair ? (masked ? MX_LAUNCH(128, true, 2) : MX_LAUNCH(128, false, 2))
+               : (masked ? MX_LAUNCH(128, true, 1) : MX_LAUNCH(128, false, 1));
       break;
-    default:
-      e = masked ? MX_LAUNCH(256, true) : MX_LAUNCH(256, false);
+    default:  // head_dim 256: single tiles only
+      e = masked ? MX_LAUNCH(256, true, 1) : MX_LAUNCH(256, false, 1);
       break;
   }
 #undef MX_LAUNCH

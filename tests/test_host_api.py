@@ -103,7 +103,7 @@ def test_null_pointers_are_rejected(field):
     (dict(SQ=0), _lib.MX_STATUS_INVALID_SHAPE),
     (dict(B=300, SQ=300), _lib.MX_STATUS_UNSUPPORTED),    # combine grid: batch * seqlen_q
     (dict(causal=2), _lib.MX_STATUS_INVALID_ARGUMENT),
-    (dict(ns=-3, B=512, Hkv=8, Hq=128, SQ=4), _lib.MX_STATUS_UNSUPPORTED),  # 16384 units
+    (dict(ns=-3, B=512, Hkv=8, Hq=128, SQ=8), _lib.MX_STATUS_UNSUPPORTED),  # 16384 units
     (dict(phase=3), _lib.MX_STATUS_INVALID_ARGUMENT),
     (dict(scale=float("nan")), _lib.MX_STATUS_INVALID_ARGUMENT),
     (dict(scale=float("inf")), _lib.MX_STATUS_INVALID_ARGUMENT),
@@ -223,27 +223,27 @@ def test_policy_on_the_north_star_configs():
         assert (p["workgroups"] if sched == "balanced" else p["splits"]) == n, name
 
 
-@pytest.mark.parametrize("SQ,Hq,Hkv,tiles", [
-    (1, 32, 8, 1), (4, 32, 8, 1), (5, 32, 8, 2), (8, 64, 8, 4), (16, 8, 8, 1), (17, 8, 8, 2),
-    (3, 28, 4, 2),
+@pytest.mark.parametrize("SQ,Hq,Hkv,D,groups,group_rows", [
+    (1, 32, 8, 128, 1, 4), (4, 32, 8, 128, 1, 16), (5, 32, 8, 128, 1, 20), (8, 64, 8, 128, 2, 32),
+    (16, 8, 8, 128, 1, 16), (17, 8, 8, 128, 1, 17), (3, 28, 4, 64, 1, 21),
+    (5, 32, 8, 256, 2, 16),    # head_dim 256: single 16-row tiles only
 ])
-def test_multi_token_row_tiles(SQ, Hq, Hkv, tiles):
-    """seqlen_q * group query rows per KV head run in tiles of 16: the split grid launches
-    Hkv * tiles workgroups per (sequence, split), its partial rows are per (token, head), and
-    the balanced schedule counts units per (sequence, KV head, tile)."""
-    G = Hq // Hkv
-    assert tiles == math.ceil(SQ * G / 16)
-    p = plan(2, Hq, Hkv, 128, 16, 64, 0, 3, num_cus=256, seqlen_q=SQ)
+def test_multi_token_row_groups(SQ, Hq, Hkv, D, groups, group_rows):
+    """seqlen_q * group query rows per KV head run in row groups: one 16-row tile, or (above
+    16 rows, head_dim <= 128) two tiles sharing each pass over K/V.  The split grid launches
+    Hkv * groups workgroups per (sequence, split), its partial rows are per (token, head), and
+    the balanced schedule counts one unit per (sequence, KV head, row group) with partial
+    slots of min(rows, rows per group) rows."""
+    p = plan(2, Hq, Hkv, D, 16, 64, 0, 3, num_cus=256, seqlen_q=SQ)
     assert p["schedule"] == "split_grid" and p["splits"] == 3
-    assert p["workgroups"] == 2 * Hkv * tiles * 3
+    assert p["workgroups"] == 2 * Hkv * groups * 3
     rows = 2 * SQ * Hq * 3
-    assert p["workspace_bytes"] == PARTIAL_BASE + math.ceil(rows * 4 / 256) * 256 + rows * 128 * 4
-    b = plan(64, Hq, Hkv, 128, 16, 64, 0, -100, num_cus=256, seqlen_q=SQ)
-    slots = 100 + 64 * Hkv * tiles
-    tr = min(16, SQ * G)
+    assert p["workspace_bytes"] == PARTIAL_BASE + math.ceil(rows * 4 / 256) * 256 + rows * D * 4
+    b = plan(64, Hq, Hkv, D, 16, 64, 0, -100, num_cus=256, seqlen_q=SQ)
+    slots = 100 + 64 * Hkv * groups
     assert b["schedule"] == "balanced"
-    assert b["workspace_bytes"] == (PARTIAL_BASE + math.ceil(slots * tr * 4 / 256) * 256
-                                    + slots * tr * 128 * 4)
+    assert b["workspace_bytes"] == (PARTIAL_BASE + math.ceil(slots * group_rows * 4 / 256) * 256
+                                    + slots * group_rows * D * 4)
 
 
 @pytest.mark.skipif(gpu_available(), reason="would launch on the fake pointers")
