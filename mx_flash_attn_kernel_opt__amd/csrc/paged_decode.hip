@@ -395,6 +395,7 @@ struct MainShape {
   // split grid
   int num_splits;
   int tokens_per_split;  // multiple of page_size
+  int fused_combine;     // split grid: the last split of each unit merges the partials itself
   // balanced schedule
   int num_groups;        // workgroups of the launch
   int unit_overhead;     // positions charged per (sequence, KV head) on top of its chunks
@@ -653,95 +654,7 @@ __device__ __forceinline__ void setup_row_group(bf16x8 (&qop)[KT][D / 32],
   }
 }
 
-// ------------------------------------------------------------------------------------------
-// Split-grid kernel
-// ------------------------------------------------------------------------------------------
-
-// Grid (Hkv * row_tiles, batch, splits), NW waves per workgroup, row_tiles groups of KT 16-row
-// tiles per KV head.  Consecutive workgroup ids, which the dispatcher deals round-robin to the
-// 8 XCDs, walk the KV heads (and row groups) of one sequence first, then the sequences, then
-// the splits.  Every XCD therefore gets an even share of the first split of every sequence
-// (where ragged batches keep most of their work), and the workgroups that read the same
-// physical pages start together.
-//
-// The NW waves of a workgroup share one (KV head, row group, sequence, split): wave wv streams
-// chunks c0+wv, c0+wv+NW, ... through its own register ring (so NW times more K/V bytes are in
-// flight per split, with no global partials), and the waves merge their (m, l, O) states
-// through LDS.  KT = 2 holds two tiles' states per wave, so one wave per SIMD (512 registers).
-template <int D, int NBUF, int NW, bool kCausal, int KT>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
-    KT == 2 ? 1 : (D == 64 ? MX_WAVES_PER_EU_D64 : (D == 128 ? MX_WAVES_PER_EU_D128 : MX_WAVES_PER_EU_D256)))))
-void mx_paged_decode_splitkv(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
-    const uint16_t* __restrict__ vc, uint16_t* __restrict__ out,
-    const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ block_table,
-    float* __restrict__ part_o, float* __restrict__ part_lse, uint32_t* __restrict__ status,
-    const MainShape sh) {
-  using L = GroupLds<D, NW, KT>;
-  __shared__ __attribute__((aligned(16))) char lds[L::kBytes];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  // Wave index, made provably wave-uniform so the chunk indices derived from it stay in
-  // SGPRs and the page lookups remain scalar loads (off the vector-memory counter).
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kv = blockIdx.x / sh.row_tiles;
-  const int grp = blockIdx.x - kv * sh.row_tiles;  // row group: rows grp*16*KT ..
-  const int r0 = grp * 16 * KT;
-  const int b = blockIdx.y;
-  const int split = blockIdx.z;
-  const int nrows = min(16 * KT, sh.rows - r0);  // query rows of this group
-
-  const int seq = clamped_len(seq_lens, b, sh, status, split == 0 && blockIdx.x == 0 && tid == 0);
-  if (seq <= 0) {
-    // Empty sequence: defined as a zero output.
-    if (split == 0)
-      for (int e = tid; e < nrows * (D / 4); e += 64 * NW)
-        store_bf16x4(out + (row_base(b, kv, sh) + row_offset(r0 + e / (D / 4), sh)) * D +
-                         4 * (e % (D / 4)),
-                     f32x4{0.f, 0.f, 0.f, 0.f});
-    return;
-  }
-  const int t0 = split * sh.tokens_per_split;
-  if (t0 >= seq) return;  // uniform over the workgroup: no barrier is skipped by part of it
-  const int t1 = min(t0 + sh.tokens_per_split, seq);
-  const bool single = seq <= sh.tokens_per_split;
-  const int c_last = (seq - 1) / kChunk;
-  // First chunk any row of this group must mask (causal), else the last chunk.
-  const int c_mask =
-      kCausal ? min(c_last, max(0, row_key_limit(r0, seq, sh)) / kChunk) : c_last;
-
-  bf16x8 qop[KT][D / 32];
-  SoftmaxState<D> st[KT];
-  int row_lim[KT];
-  setup_row_group<D, KT>(qop, st, row_lim, q, b, kv, grp, seq, sh, lane);
-  bool bad_page = false;
-  stream_chunks<D, NBUF, NW, kCausal, KT>(st, qop, kc, vc,
-                                          block_table + (int64_t)b * sh.max_pages, kv,
-                                          t0 / kChunk, (t1 + kChunk - 1) / kChunk, seq, c_mask,
-                                          row_lim, wv, L::ktile(lds, wv), sh, bad_page);
-  if (bad_page && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
-  publish_wave_state<D, NW, KT>(lds, st, wv);
-  for (int e = tid; e < nrows * (D / 4); e += 64 * NW) {
-    const int hh = e / (D / 4);
-    const int d = 4 * (e - hh * (D / 4));
-    float lse;
-    const f32x4 o = merged_head<D, NW, KT>(lds, hh, d, lse);
-    const int64_t row = row_base(b, kv, sh) + row_offset(r0 + hh, sh);
-    if (single) {
-      store_bf16x4(out + row * D + d, o);
-    } else {
-      *reinterpret_cast<f32x4*>(part_o + (row * sh.num_splits + split) * D + d) = o;
-      if (d == 0) part_lse[row * sh.num_splits + split] = lse;
-    }
-  }
-}
-
-// ------------------------------------------------------------------------------------------
-// Length-balanced kernel
-// ------------------------------------------------------------------------------------------
-
-constexpr int kMergeFanIn = 8;   // partials merged per step of the cross-workgroup merge tree
-constexpr int kMergeLevels = 4;  // enough for 8^4 = 4096 pieces per unit
+constexpr int kMergeFanIn = 8;   // partials merged per step of a cross-workgroup merge
 
 // Cross-workgroup handoff of partials.  Device-scoped accesses (MX_MERGE_SCOPED_ACCESS = 1):
 // partials are stored and loaded with agent-scope atomic accesses (write-through / coherent at
@@ -808,6 +721,158 @@ __device__ __forceinline__ void acquire_partials() {
   __threadfence();
 #endif
 }
+
+// ------------------------------------------------------------------------------------------
+// Split-grid kernel
+// ------------------------------------------------------------------------------------------
+
+// Grid (Hkv * row_tiles, batch, splits), NW waves per workgroup, row_tiles groups of KT 16-row
+// tiles per KV head.  Consecutive workgroup ids, which the dispatcher deals round-robin to the
+// 8 XCDs, walk the KV heads (and row groups) of one sequence first, then the sequences, then
+// the splits.  Every XCD therefore gets an even share of the first split of every sequence
+// (where ragged batches keep most of their work), and the workgroups that read the same
+// physical pages start together.
+//
+// The NW waves of a workgroup share one (KV head, row group, sequence, split): wave wv streams
+// chunks c0+wv, c0+wv+NW, ... through its own register ring (so NW times more K/V bytes are in
+// flight per split, with no global partials), and the waves merge their (m, l, O) states
+// through LDS.  KT = 2 holds two tiles' states per wave, so one wave per SIMD (512 registers).
+//
+// A sequence cut into several splits leaves one normalised partial (O/l, log2-sum-exp) per
+// split and row.  With fused_combine the last split of each unit to finish (a device-scope
+// arrival counter per unit) merges them itself, so the whole call is one launch; otherwise
+// mx_paged_decode_combine merges them in a second launch.
+template <int D, int NBUF, int NW, bool kCausal, int KT>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
+    KT == 2 ? 1 : (D == 64 ? MX_WAVES_PER_EU_D64 : (D == 128 ? MX_WAVES_PER_EU_D128 : MX_WAVES_PER_EU_D256)))))
+void mx_paged_decode_splitkv(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, uint16_t* __restrict__ out,
+    const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ block_table,
+    float* __restrict__ part_o, float* __restrict__ part_lse, uint32_t* __restrict__ counters,
+    uint32_t* __restrict__ status, const MainShape sh) {
+  using L = GroupLds<D, NW, KT>;
+  __shared__ __attribute__((aligned(16))) char lds[L::kBytes];
+  __shared__ int s_last;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  // Wave index, made provably wave-uniform so the chunk indices derived from it stay in
+  // SGPRs and the page lookups remain scalar loads (off the vector-memory counter).
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kv = sh.row_tiles == 1 ? (int)blockIdx.x : (int)blockIdx.x / sh.row_tiles;
+  const int grp = blockIdx.x - kv * sh.row_tiles;  // row group: rows grp*16*KT ..
+  const int r0 = grp * 16 * KT;
+  const int b = blockIdx.y;
+  const int split = blockIdx.z;
+  const int nrows = min(16 * KT, sh.rows - r0);  // query rows of this group
+
+  const int seq = clamped_len(seq_lens, b, sh, status, split == 0 && blockIdx.x == 0 && tid == 0);
+  if (seq <= 0) {
+    // Empty sequence: defined as a zero output.
+    if (split == 0)
+      for (int e = tid; e < nrows * (D / 4); e += 64 * NW)
+        store_bf16x4(out + (row_base(b, kv, sh) + row_offset(r0 + e / (D / 4), sh)) * D +
+                         4 * (e % (D / 4)),
+                     f32x4{0.f, 0.f, 0.f, 0.f});
+    return;
+  }
+  const int t0 = split * sh.tokens_per_split;
+  if (t0 >= seq) return;  // uniform over the workgroup: no barrier is skipped by part of it
+  const int t1 = min(t0 + sh.tokens_per_split, seq);
+  const bool single = seq <= sh.tokens_per_split;
+  const int c_last = (seq - 1) / kChunk;
+  // First chunk any row of this group must mask (causal), else the last chunk.
+  const int c_mask =
+      kCausal ? min(c_last, max(0, row_key_limit(r0, seq, sh)) / kChunk) : c_last;
+
+  bf16x8 qop[KT][D / 32];
+  SoftmaxState<D> st[KT];
+  int row_lim[KT];
+  setup_row_group<D, KT>(qop, st, row_lim, q, b, kv, grp, seq, sh, lane);
+  bool bad_page = false;
+  stream_chunks<D, NBUF, NW, kCausal, KT>(st, qop, kc, vc,
+                                          block_table + (int64_t)b * sh.max_pages, kv,
+                                          t0 / kChunk, (t1 + kChunk - 1) / kChunk, seq, c_mask,
+                                          row_lim, wv, L::ktile(lds, wv), sh, bad_page);
+  if (bad_page && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
+  publish_wave_state<D, NW, KT>(lds, st, wv);
+  for (int e = tid; e < nrows * (D / 4); e += 64 * NW) {
+    const int hh = e / (D / 4);
+    const int d = 4 * (e - hh * (D / 4));
+    float lse;
+    const f32x4 o = merged_head<D, NW, KT>(lds, hh, d, lse);
+    const int64_t row = row_base(b, kv, sh) + row_offset(r0 + hh, sh);
+    if (single) {
+      store_bf16x4(out + row * D + d, o);
+    } else if (sh.fused_combine) {  // read back by another workgroup of this launch
+      store_partial4(part_o + (row * sh.num_splits + split) * D + d, o);
+      if (d == 0) store_partial1(part_lse + row * sh.num_splits + split, lse);
+    } else {                        // read by the combine kernel of the next launch
+      *reinterpret_cast<f32x4*>(part_o + (row * sh.num_splits + split) * D + d) = o;
+      if (d == 0) part_lse[row * sh.num_splits + split] = lse;
+    }
+  }
+  if (single || !sh.fused_combine) return;
+
+  // Arrival of this split; the unit's last split merges all of them.
+  const int nsv = (seq + sh.tokens_per_split - 1) / sh.tokens_per_split;  // splits with tokens
+  uint32_t* counter = counters + (int64_t)b * gridDim.x + blockIdx.x;
+  publish_partials();
+  __syncthreads();
+  if (tid == 0) s_last = (atomicAdd(counter, 1u) == (uint32_t)(nsv - 1)) ? 1 : 0;
+  __syncthreads();
+  if (!s_last) return;
+  if (tid == 0) *counter = 0u;  // ready for the next call
+  acquire_partials();
+  // out[row] = sum_s 2^(lse_s - M) O_s / sum_s 2^(lse_s - M), M = max_s lse_s; a causal row no
+  // split saw a key for (every lse -inf) stays zeros.
+  // One online pass, the loads of kMergeFanIn splits issued together per round.
+  for (int e = tid; e < nrows * (D / 4); e += 64 * NW) {
+    const int hh = e / (D / 4);
+    const int d = 4 * (e - hh * (D / 4));
+    const int64_t row = row_base(b, kv, sh) + row_offset(r0 + hh, sh);
+    const float* lse = part_lse + row * sh.num_splits;
+    const float* po = part_o + row * sh.num_splits * D + d;
+    float mx = -INFINITY;  // running max of the log2-sum-exps seen
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    float wsum = 0.f;
+    for (int s0 = 0; s0 < nsv; s0 += kMergeFanIn) {
+      float ls[kMergeFanIn];
+      f32x4 vs[kMergeFanIn];
+#pragma unroll
+      for (int t = 0; t < kMergeFanIn; ++t) {  // unconditional loads, extra slots masked
+        const int sl = min(s0 + t, nsv - 1);
+        ls[t] = load_partial1(lse + sl);
+        vs[t] = load_partial4(po + (int64_t)sl * D);
+      }
+#pragma unroll
+      for (int t = 0; t < kMergeFanIn; ++t)
+        if (s0 + t >= nsv) ls[t] = -INFINITY;
+      float bm = mx;
+#pragma unroll
+      for (int t = 0; t < kMergeFanIn; ++t) bm = fmaxf(bm, ls[t]);
+      if (bm > -INFINITY) {
+        const float a = __builtin_amdgcn_exp2f(mx - bm);  // 0 while nothing was seen
+        acc *= a;
+        wsum *= a;
+#pragma unroll
+        for (int t = 0; t < kMergeFanIn; ++t) {
+          const float w = __builtin_amdgcn_exp2f(ls[t] - bm);
+          wsum += w;
+          acc += w * vs[t];
+        }
+        mx = bm;
+      }
+    }
+    store_bf16x4(out + row * D + d, acc * (wsum > 0.f ? 1.0f / wsum : 0.f));
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Length-balanced kernel
+// ------------------------------------------------------------------------------------------
+
+constexpr int kMergeLevels = 4;  // enough for 8^4 = 4096 pieces per unit
 
 // Block-wide sum of one int per thread (all threads get the result).
 template <int NW>
@@ -1021,12 +1086,14 @@ void mx_paged_decode_balanced(
             float lses[kMergeFanIn];
             f32x4 vals[kMergeFanIn];
 #pragma unroll
-            for (int t = 0; t < kMergeFanIn; ++t) {
-              const int64_t sl = gslot + t * stride;
-              lses[t] = t < gsize ? load_partial1(part_lse + sl * TR + hh) : -INFINITY;
-              vals[t] = t < gsize ? load_partial4(part_o + (sl * TR + hh) * D + d)
-                                  : f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int t = 0; t < kMergeFanIn; ++t) {  // unconditional loads, extra slots masked
+              const int64_t sl = gslot + min(t, gsize - 1) * stride;
+              lses[t] = load_partial1(part_lse + sl * TR + hh);
+              vals[t] = load_partial4(part_o + (sl * TR + hh) * D + d);
             }
+#pragma unroll
+            for (int t = 0; t < kMergeFanIn; ++t)
+              if (t >= gsize) lses[t] = -INFINITY;
 #pragma unroll
             for (int t = 0; t < kMergeFanIn; ++t) mx = fmaxf(mx, lses[t]);
             // A row no piece of the group saw a key for (every lse -inf) stays zeros with
@@ -1101,36 +1168,58 @@ __global__ __launch_bounds__(64) void mx_paged_decode_combine(
   const float* lse = part_lse + row * num_splits;
   const float* po = part_o + row * num_splits * D + E * lane;
 
-  float mx = -INFINITY;
-  for (int s = lane; s < nsv; s += 64) mx = fmaxf(mx, lse[s]);
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-
+  // One online pass over the splits, the loads of kCombineBatch splits issued together per
+  // round (the pass is latency-bound: a row's partials are a few KB).
+  constexpr int kCombineBatch = 16;
+  float mx = -INFINITY;  // running max of the log2-sum-exps seen
   float acc[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) acc[e] = 0.f;
   float wsum = 0.f;
-  if (mx == -INFINITY) {
-    mx = 0.f;      // no split saw a key: every weight below is 0
-    wsum = 1.f;    // and the output zeros
-  }
-#pragma unroll 4
-  for (int s = 0; s < nsv; ++s) {
-    const float w = __builtin_amdgcn_exp2f(lse[s] - mx);
-    wsum += w;
-    const float* src = po + (int64_t)s * D;
-    if constexpr (E == 1) {
-      acc[0] += w * src[0];
-    } else if constexpr (E == 2) {
-      const f32x2 x = *reinterpret_cast<const f32x2*>(src);
-      acc[0] += w * x[0];
-      acc[1] += w * x[1];
-    } else {
-      const f32x4 x = *reinterpret_cast<const f32x4*>(src);
+  for (int s0 = 0; s0 < nsv; s0 += kCombineBatch) {
+    float ls[kCombineBatch];
+    float vs[kCombineBatch][E];
+    // Every slot loads (past the last split it re-reads the last one), so the loads are
+    // unconditional and issue back to back; the extra slots are masked by their lse below.
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[e] += w * x[e];
+    for (int t = 0; t < kCombineBatch; ++t) {
+      const int sl = min(s0 + t, nsv - 1);
+      ls[t] = lse[sl];
+      const float* src = po + (int64_t)sl * D;
+      if constexpr (E == 1) {
+        vs[t][0] = src[0];
+      } else if constexpr (E == 2) {
+        const f32x2 x = *reinterpret_cast<const f32x2*>(src);
+        vs[t][0] = x[0];
+        vs[t][1] = x[1];
+      } else {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(src);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vs[t][e] = x[e];
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < kCombineBatch; ++t)
+      if (s0 + t >= nsv) ls[t] = -INFINITY;
+    float bm = mx;
+#pragma unroll
+    for (int t = 0; t < kCombineBatch; ++t) bm = fmaxf(bm, ls[t]);
+    if (bm > -INFINITY) {  // else: no split so far saw a key for this row
+      const float a = __builtin_amdgcn_exp2f(mx - bm);
+      wsum *= a;
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[e] *= a;
+#pragma unroll
+      for (int t = 0; t < kCombineBatch; ++t) {
+        const float w = __builtin_amdgcn_exp2f(ls[t] - bm);
+        wsum += w;
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[e] += w * vs[t][e];
+      }
+      mx = bm;
     }
   }
+  if (!(wsum > 0.f)) wsum = 1.f;  // a row no split saw a key for: zeros
   const float inv = 1.0f / wsum;
   uint16_t* op = out + row * D + E * lane;
   if constexpr (E == 1) {
@@ -1219,6 +1308,7 @@ constexpr int64_t kMinTokensPerSplit = 128;   // amortises Q load, pipeline fill
 constexpr int64_t kMaxTokensPerSplit = 16384;  // bounds one workgroup's share of a sequence
 constexpr int64_t kMaxGridDim = 65535;
 constexpr int64_t kBalancedMinUnits = 64;
+constexpr int64_t kFusedMaxSplits = 16;  // split grid: merge in-kernel up to this many splits
 
 int64_t groups_per_cu(int64_t head_dim) { return head_dim == 64 ? 2 : 1; }
 
@@ -1456,6 +1546,7 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   sh.cap_tokens = (int)plan.cap_tokens;
   sh.scale_log2 = scale * 1.4426950408889634f;
   sh.num_splits = (int)plan.splits;
+  sh.fused_combine = 0;
   sh.tokens_per_split = (int)plan.tokens_per_split;
   sh.num_groups = (int)plan.groups;
   sh.unit_overhead = MX_UNIT_OVERHEAD;
@@ -1478,17 +1569,26 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
 
   float* part_lse = plan.splits > 1 ? reinterpret_cast<float*>(ws + plan.lse_offset) : nullptr;
   float* part_o = plan.splits > 1 ? reinterpret_cast<float*>(ws + plan.o_offset) : nullptr;
+  // One launch (the last split of each unit merges) for up to kFusedMaxSplits splits, when the
+  // units' arrival counters fit the counter region and the caller did not ask for the two
+  // phases separately.  With more splits the merging workgroup's chain of rounds costs more
+  // than a second launch whose many workgroups merge rows in parallel (measured: tiny 10.3 ->
+  // 8.9 us fused at 4 splits; 64 splits 31.1 -> 33.0 us).
+  const bool fused = phase == 0 && plan.splits > 1 && plan.splits <= kFusedMaxSplits &&
+                     batch * num_kv_heads * plan.row_tiles <= kMaxSlots;
+  sh.fused_combine = fused ? 1 : 0;
   if (phase != MX_PHASE_COMBINE_ONLY) {
     const dim3 grid((unsigned)(num_kv_heads * plan.row_tiles), (unsigned)batch,
                     (unsigned)plan.splits);
     hipLaunchKernelGGL((mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT>), grid, dim3(64 * kNW), 0,
                        stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                        static_cast<const uint16_t*>(v), static_cast<uint16_t*>(out), seq_lens,
-                       block_table, part_o, part_lse, status, sh);
+                       block_table, part_o, part_lse,
+                       reinterpret_cast<uint32_t*>(ws + kStatusBytes), status, sh);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  if (phase != MX_PHASE_MAIN_ONLY && plan.splits > 1) {
+  if (phase != MX_PHASE_MAIN_ONLY && plan.splits > 1 && !fused) {
     const dim3 grid((unsigned)num_heads, (unsigned)(batch * seqlen_q));
     hipLaunchKernelGGL(mx_paged_decode_combine<D>, grid, dim3(64), 0, stream, part_o, part_lse,
                        seq_lens, static_cast<uint16_t*>(out), (int)num_heads, (int)seqlen_q,

@@ -441,3 +441,40 @@ def test_single_token_causal_equals_non_causal():
     a = _decode(inp, causal=False).clone()
     b = _decode(inp, causal=True)
     assert torch.equal(a, b)
+
+
+# ------------------------------------------------------------------------------------------
+# Split grid: in-kernel merge by the last split (one launch) vs the two-phase form
+# ------------------------------------------------------------------------------------------
+
+def test_split_grid_fused_merge_matches_two_phase_combine():
+    """phase 0 merges the splits inside the main kernel (last split of each unit); the
+    MX_PHASE_MAIN_ONLY + MX_PHASE_COMBINE_ONLY pair runs the separate combine kernel."""
+    from mx_flash_attn_kernel_opt__amd import _lib, make_workspace, plan
+
+    spec = W.custom_spec("fuse", RAGGED_LENS, 32, 8, 128, 16)
+    inp = W.make_inputs(spec, seed=21, device=DEV)
+    p = plan(spec.batch, 32, 8, 128, 16, spec.max_pages, 0, 7)
+    assert p["schedule"] == "split_grid" and p["splits"] > 1
+    ws = make_workspace(p["workspace_bytes"], DEV)
+    fused = _decode(inp, num_splits=7, workspace=ws).clone()
+    two = torch.empty_like(fused)
+    paged_gqa_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_table, inp.seq_lens, inp.scale,
+                     out=two, num_splits=7, workspace=ws, phase=_lib.MX_PHASE_MAIN_ONLY)
+    paged_gqa_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_table, inp.seq_lens, inp.scale,
+                     out=two, num_splits=7, workspace=ws, phase=_lib.MX_PHASE_COMBINE_ONLY)
+    torch.cuda.synchronize()
+    _check(inp, fused, label="fused merge")
+    _check(inp, two, label="two-phase combine")
+    assert (fused.float() - two.float()).abs().max().item() <= 1e-2
+    again = _decode(inp, num_splits=7, workspace=ws)     # counters were reset by the merges
+    assert torch.equal(again, fused)
+
+
+def test_split_grid_with_more_units_than_counters_uses_the_combine_kernel():
+    """batch * Hkv above the 12 288 arrival counters falls back to the second launch."""
+    B = 1600
+    spec = W.custom_spec("many", [40 + (b % 7) for b in range(B)], 16, 8, 64, 16)
+    inp = W.make_inputs(spec, seed=22, device=DEV)
+    out = _decode(inp, num_splits=2)
+    _check(inp, out, batches=_sample(B, 40), label="many units, split 2")
