@@ -1,7 +1,7 @@
 """Benchmark of the paged GQA decode operator on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload llama3_8b]
-                    [--num-splits 0] [--no-cpu-baseline] [--all]
+                    [--num-splits 0] [--no-cpu-baseline] [--all] [--shards N]
 
 One step = one decode-attention call over the whole batch of the workload (default: the
 Llama-3-8B decode shape the metric is quoted on, B=64 Hq=32 Hkv=8 D=128 P=16 L=4096), inputs
@@ -14,6 +14,8 @@ after the second event).  Prints ONE JSON line:
   cpu_baseline  the fp32 oracle (oracle/paged_attention.py) timed on this host on a bounded
              sample of the same workload.
 ``--all`` prints one extra JSON line per north-star configuration (no CPU baseline).
+``--shards N`` prints one extra line: the workload's pages cut into N shards, each shard's
+partial decode and the N-way merge timed on this GPU (the per-GPU work of an N-GPU decode).
 """
 
 from __future__ import annotations
@@ -83,36 +85,44 @@ def time_workload(inp: W.DecodeInputs, steps: int, warmup: int, num_splits: int 
                              causal=spec.causal, num_splits=num_splits, workspace=ws,
                              stream=stream)
              for k, v in pools]
-    split = plan["splits"] > 1
-    main_phase = _lib.MX_PHASE_MAIN_ONLY if split else _lib.MX_PHASE_ALL
+    # A call that launches two kernels (split grid, many splits) is issued as its two phases
+    # so the events bracket the main kernel alone; a one-launch call is issued as is.
+    two = plan["launches"] == 2
+    main_phase = _lib.MX_PHASE_MAIN_ONLY if two else _lib.MX_PHASE_ALL
 
-    def step(i, e0=None, e1=None):
-        call = calls[i % len(calls)]
+    def step(call, e0=None, e1=None):
         if e0 is not None:
             e0.record(stream)
         call(main_phase)
         if e1 is not None:
             e1.record(stream)
-        if split:
+        if two:
             call(_lib.MX_PHASE_COMBINE_ONLY)
 
+    def timed(pick):
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record(stream)
+        for i in range(steps):
+            step(pick(i), *ev[i])
+        end.record(stream)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3 / steps
+        return start.elapsed_time(end) / steps, [a.elapsed_time(b) * 1e3 for a, b in ev], wall
+
     for i in range(warmup):
-        step(i)
-    torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    start.record(stream)
-    for i in range(steps):
-        step(i, *ev[i])
-    end.record(stream)
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3
-    total_ms = start.elapsed_time(end)
-    kern_us = [a.elapsed_time(b) * 1e3 for a, b in ev]
-    ms_per_step = total_ms / steps
+        step(calls[i % len(calls)])
+    ms_per_step, kern_us, wall_ms_step = timed(lambda i: calls[i % len(calls)])
+    warm = None
+    if copies > 1:
+        # The same calls on one pool only: after the first, its K/V is served from the MALL.
+        w_ms, w_kern, _ = timed(lambda i: calls[0])
+        warm = {"us_per_call": round(w_ms * 1e3, 2),
+                "kernel_us_mean": round(statistics.fmean(w_kern), 2),
+                "GBps": round(nbytes / (w_ms * 1e-3) / 1e9, 1)}
     flags = pkg.read_device_status(ws)
     if flags:
         raise RuntimeError(f"device status flags {flags} raised during the benchmark")
@@ -121,7 +131,8 @@ def time_workload(inp: W.DecodeInputs, steps: int, warmup: int, num_splits: int 
         "nbytes": nbytes,
         "plan": plan,
         "ms_per_step": ms_per_step,
-        "wall_ms_per_step": wall_ms / steps,
+        "wall_ms_per_step": wall_ms_step,
+        "warm": warm,
         "kernel_us_mean": kern_mean,
         "kernel_us_median": statistics.median(kern_us),
         "kernel_us_min": min(kern_us),
@@ -178,6 +189,86 @@ def time_append(spec: W.DecodeSpec, steps: int, warmup: int, seed: int = 0) -> d
                        "num_kv_heads": Hkv, "head_dim": D, "page_size": spec.page_size},
             "bytes_per_call": nbytes, "GBps": round(nbytes / us / 1e3, 2),
             "note": "launch-bound: one token per sequence moves bytes_per_call"}
+
+
+def time_shards(inp: W.DecodeInputs, num_shards: int, steps: int, warmup: int) -> dict:
+    """The per-GPU pieces of a sharded decode of `inp`, all run on this one GPU: each shard's
+    partial decode (shard_pages layout; calls rotate over the shards so no shard is served
+    from the MALL by its previous call) and the merge of the num_shards partials."""
+    spec = inp.spec
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    lib = _lib.load()
+    shards = pkg.shard_pages(inp.block_table, inp.seq_lens, spec.page_size, num_shards,
+                             spec.seqlen_q)
+    B, SQ, Hq, Hkv, D = spec.batch, spec.seqlen_q, spec.num_heads, spec.num_kv_heads, spec.head_dim
+    P, width = spec.page_size, inp.block_table.shape[1]
+    lens_host = [s[1].cpu() for s in shards]
+    # Plan each shard for the keys it holds (max_seq_len), as its own GPU would.
+    caps = [max(int(lh.max()), 1) for lh in lens_host]
+    need = max(pkg.workspace_size(B, Hq, Hkv, D, P, width, cap, 0, seqlen_q=SQ) for cap in caps)
+    ws = pkg.make_workspace(need, inp.device)
+    o = torch.empty((num_shards,) + tuple(inp.q.shape), dtype=torch.float32, device=inp.device)
+    lse = torch.empty(o.shape[:-1], dtype=torch.float32, device=inp.device)
+    out = torch.empty_like(inp.q)
+    P_ = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    args = []
+    for s, (table, lens) in enumerate(shards):
+        causal = int(spec.causal and s == num_shards - 1)
+        pkg.paged_gqa_decode_partial(inp.q, inp.k_cache, inp.v_cache, table, lens, inp.scale,
+                                     causal=bool(causal), max_seq_len=caps[s], workspace=ws)
+        args.append([P_(inp.q), P_(inp.k_cache), P_(inp.v_cache), P_(o[s]), P_(lse[s]),
+                     P_(lens), P_(table), B, SQ, Hq, Hkv, D, P, inp.k_cache.shape[0], width,
+                     caps[s], causal, float(inp.scale), 0, P_(ws), ws.numel(), sp])
+    merge_args = [P_(o), P_(lse), num_shards, B * SQ * Hq, D, P_(out), sp]
+
+    def partial(s):
+        st = lib.mx_paged_gqa_decode_partial(*args[s])
+        if st != _lib.MX_STATUS_OK:
+            _lib.check(st)
+
+    def merge():
+        st = lib.mx_lse_merge(*merge_args)
+        if st != _lib.MX_STATUS_OK:
+            _lib.check(st)
+
+    for i in range(warmup):
+        partial(i % num_shards)
+        merge()
+    torch.cuda.synchronize()
+    ev_p = [[] for _ in range(num_shards)]
+    ev_m = []
+    for i in range(steps):
+        for s in range(num_shards):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            partial(s)
+            b.record(stream)
+            ev_p[s].append((a, b))
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        merge()
+        b.record(stream)
+        ev_m.append((a, b))
+    torch.cuda.synchronize()
+    if pkg.read_device_status(ws):
+        raise RuntimeError("device status flags raised during the shard benchmark")
+    per_shard = [statistics.median(a.elapsed_time(b) * 1e3 for a, b in ev) for ev in ev_p]
+    merge_us = statistics.median(a.elapsed_time(b) * 1e3 for a, b in ev_m)
+    shard_bytes = [int(lh.clamp(min=0).sum()) * Hkv * D * 4 for lh in lens_host]
+    worst = max(range(num_shards), key=lambda s: per_shard[s])
+    return {
+        "metric": "sharded_decode_per_gpu_us", "value": round(per_shard[worst] + merge_us, 2),
+        "unit": "us", "higher_is_better": False, "n_gpus": 1, "steps": steps, "dtype": "bf16",
+        "config": {"workload": spec.name, "shards": num_shards,
+                   "shard_tokens": [int(lh.clamp(min=0).sum()) for lh in lens_host]},
+        "partial_us": [round(x, 2) for x in per_shard],
+        "partial_GBps": [round(b / t / 1e3, 1) for b, t in zip(shard_bytes, per_shard)],
+        "merge_us": round(merge_us, 2),
+        "note": ("value = slowest shard's partial decode + the merge, the work of one GPU of a "
+                 "num_shards-GPU job; the all-gather of (o, lse) between them is not measured "
+                 "(one GPU)"),
+    }
 
 
 # The reference's contest score model (archive/round_deepnight/agentC_policy_NOTES.md:17-27):
@@ -237,31 +328,42 @@ def cpu_baseline(inp: W.DecodeInputs, budget_s: float) -> dict:
     threads = torch.get_num_threads()
     B = inp.spec.batch
     order = torch.randperm(B, generator=torch.Generator().manual_seed(0)).tolist()
-    warm = inp.subset([order[0]])
-    paged_decode_reference(warm.q, warm.k_cache, warm.v_cache, warm.block_table,
-                           warm.seq_lens, warm.scale)
-    spent, nbytes, done = 0.0, 0, 0
+    subs = []
+
+    def run(sub):
+        paged_decode_reference(sub.q, sub.k_cache, sub.v_cache, sub.block_table, sub.seq_lens,
+                               sub.scale)
+
+    # Sample: sequences in a fixed random order until one pass takes about a third of the
+    # budget (one pass also warms up); then 3 timed passes over that sample, median reported.
+    first = 0.0
     for b in order:
         sub = inp.subset([b])
         t0 = time.perf_counter()
-        paged_decode_reference(sub.q, sub.k_cache, sub.v_cache, sub.block_table,
-                               sub.seq_lens, sub.scale)
-        spent += time.perf_counter() - t0
-        nbytes += sub.kv_bytes()
-        done += 1
-        if spent >= budget_s:
+        run(sub)
+        first += time.perf_counter() - t0
+        subs.append(sub)
+        if first >= budget_s / 3:
             break
-    gbps = nbytes / spent / 1e9
+    nbytes = sum(sub.kv_bytes() for sub in subs)
+    passes = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        for sub in subs:
+            run(sub)
+        passes.append(time.perf_counter() - t0)
+    per_pass = statistics.median(passes)
+    gbps = nbytes / per_pass / 1e9
     return {
         "value": round(gbps, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"{done} of {B} sequences of {inp.spec.name}, fp32 torch oracle "
-                   f"(oracle/paged_attention.py), one sequence at a time, {spent:.1f} s; "
-                   f"host {_cpu_model()}, os.cpu_count()={os.cpu_count()}, "
-                   f"torch threads={threads}"),
-        "us_per_call_est": round(spent / done * B * 1e6, 1),
+        "sample": (f"{len(subs)} of {B} sequences of {inp.spec.name}, fp32 torch oracle "
+                   f"(oracle/paged_attention.py), one sequence at a time; median of 3 passes "
+                   f"of {per_pass:.2f} s after a warm-up pass; host {_cpu_model()}, "
+                   f"os.cpu_count()={os.cpu_count()}, torch threads={threads}"),
+        "us_per_call_est": round(per_pass / len(subs) * B * 1e6, 1),
     }
 
 
@@ -307,6 +409,10 @@ def result_line(args, spec, r, cpu=None) -> dict:
         },
         "wall_ms_per_step": round(r["wall_ms_per_step"], 5),
     }
+    if r["warm"] is not None:
+        # Cold (the value above: distinct K/V pools rotate, nothing is served from the 256 MB
+        # MALL) against warm (one pool reused).
+        line["warm"] = r["warm"]
     if cpu is not None:
         line["cpu_baseline"] = cpu
     return line
@@ -328,6 +434,9 @@ def main(argv=None) -> int:
     ap.add_argument("--suite", choices=["c500"], default=None,
                     help="run the reference's 14-case contest suite through run_kernel "
                          "instead of the main workload and print its per-case lines and score")
+    ap.add_argument("--shards", type=int, default=0,
+                    help="also time the per-GPU pieces of the workload's decode sharded over N "
+                         "GPUs' pages (partial decode per shard + merge), on this one GPU")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after timing, run 5 plain 1 GiB device copies (torch copy_) so a "
                          "rocprofv3 --pmc pass can scale FETCH_SIZE/WRITE_SIZE by a kernel of "
@@ -337,7 +446,8 @@ def main(argv=None) -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this operator is benchmarked on one GPU only; multi-GPU runs "
-              "(--gpus > 1) are not part of this build (sharding is described in DESIGN.md).",
+              "(--gpus > 1) are not part of this build; the per-GPU pieces of a sharded decode "
+              "(paged_gqa_decode_partial, lse_merge) are measured with --shards N.",
               file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
@@ -368,6 +478,10 @@ def main(argv=None) -> int:
     r = time_workload(inp, args.steps, args.warmup, args.num_splits)
     cpu = None if args.no_cpu_baseline else cpu_baseline(inp, args.cpu_budget)
     line = result_line(args, spec, r, cpu)
+    if args.shards > 0:
+        sh = time_shards(inp, args.shards, args.steps, args.warmup)
+        sh["single_gpu_us"] = line["us_per_call"]
+        print(json.dumps(sh), flush=True)
     del inp
     torch.cuda.empty_cache()
     if args.calibrate_copy:

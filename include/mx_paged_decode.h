@@ -123,6 +123,43 @@ int mx_paged_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
                         int32_t phase, void* stream);
 
 /*
+ * Partial decode of one shard of the keys (the split phase of the reference's split-KV decode,
+ * optimized_c500_flash_attn.cu:537-551 and the partial (m, l, O) rows it leaves for
+ * combine_splits, exposed for a caller-chosen key range).  Arguments as mx_paged_gqa_decode,
+ * with seq_lens / block_table describing this shard's keys only; instead of the bf16 output
+ * it writes, per query row (b, t, h):
+ *   o_partial    [batch, seqlen_q, num_heads, head_dim] fp32, 16-byte aligned: the row's
+ *                attention output over this shard's keys (normalised);
+ *   lse_partial  [batch, seqlen_q, num_heads] fp32: log(sum_t exp(scale * q . k_t)) over them.
+ * A row that sees no key of the shard (empty shard; causal rows before their first key) gets
+ * O = 0 and lse = -inf.  With causal = 1 the end-aligned mask is applied to the shard's own
+ * length, which is the global mask when the shard holds the last keys of the sequence and
+ * earlier shards end at or before L - seqlen_q + 1 (pass causal = 0 for those).  Workspace:
+ * mx_paged_gqa_decode_workspace_size of the same arguments.  Returns MX_STATUS_*.
+ */
+int mx_paged_gqa_decode_partial(const void* q, const void* k_cache, const void* v_cache,
+                                float* o_partial, float* lse_partial, const int32_t* seq_lens,
+                                const int32_t* block_table, int64_t batch, int64_t seqlen_q,
+                                int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                                int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
+                                int64_t max_seq_len, int32_t causal, float scale,
+                                int64_t num_splits, void* workspace, int64_t workspace_bytes,
+                                void* stream);
+
+/*
+ * Log-sum-exp merge of gathered partials (replaces combine_splits,
+ * optimized_c500_flash_attn.cu:666-728, over partials the caller holds, e.g. after an
+ * all-gather of every shard's mx_paged_gqa_decode_partial output):
+ *   out[r] = sum_p exp(lse[p, r] - M) o[p, r] / sum_p exp(lse[p, r] - M),  M = max_p lse[p, r].
+ *   o_parts    [num_parts, rows, head_dim] fp32, 16-byte aligned.
+ *   lse_parts  [num_parts, rows] fp32 (natural log; -inf = the part saw no key, weight 0).
+ *   out        [rows, head_dim] bf16, 8-byte aligned; a row no part saw a key for is zeros.
+ * head_dim 64, 128 or 256; rows <= 2^25.  Asynchronous on `stream`.  Returns MX_STATUS_*.
+ */
+int mx_lse_merge(const float* o_parts, const float* lse_parts, int64_t num_parts, int64_t rows,
+                 int64_t head_dim, void* out, void* stream);
+
+/*
  * Host-only planning (no HIP call when num_cus > 0): validates the shape and reports the
  * schedule (MX_SCHEDULE_*), the splits per sequence and tokens per split (split grid; 0 for the
  * balanced schedule), the workgroups launched and the workspace bytes a call with these

@@ -9,25 +9,31 @@ exposes it over PyTorch-ROCm device tensors; it has no CPU fallback.
 from ._lib import MXAttnError, library_path, load  # noqa: F401
 from .decode import (  # noqa: F401
     BoundDecode,
+    lse_merge,
     make_workspace,
     paged_gqa_decode,
+    paged_gqa_decode_partial,
     paged_kv_append,
     plan,
     read_device_status,
     run_kernel,
     workspace_size,
 )
+from .shard import shard_pages  # noqa: F401
 
 __all__ = [
     "BoundDecode",
     "MXAttnError",
     "library_path",
     "load",
+    "lse_merge",
     "make_workspace",
     "paged_gqa_decode",
+    "paged_gqa_decode_partial",
     "paged_kv_append",
     "plan",
     "read_device_status",
     "run_kernel",
+    "shard_pages",
     "workspace_size",
 ]

@@ -400,6 +400,10 @@ struct MainShape {
   int num_groups;        // workgroups of the launch
   int unit_overhead;     // positions charged per (sequence, KV head) on top of its chunks
   int num_slots;         // partial slots: num_groups + batch * Hkv
+  // Partial outputs (sharded decode): when o_out is set, each query row is written as its fp32
+  // normalised output to o_out and its natural-log sum-exp to lse_out instead of bf16 to out.
+  float* o_out;
+  float* lse_out;
 };
 
 // Sequence length as the kernels see it: clamped to the planned capacity (flagged).
@@ -639,6 +643,22 @@ __device__ __forceinline__ void store_bf16x4(uint16_t* p, f32x4 v) {
   *reinterpret_cast<u32x2*>(p) = w;
 }
 
+constexpr float kLn2 = 0.69314718055994531f;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Final output of dims d..d+3 of query row `row` with log2-sum-exp lse2: bf16 into out, or, for
+// partial outputs, fp32 into sh.o_out and (once per row) the natural-log sum-exp into sh.lse_out.
+template <int D>
+__device__ __forceinline__ void store_row4(uint16_t* out, const MainShape& sh, int64_t row, int d,
+                                           f32x4 o, float lse2) {
+  if (sh.o_out == nullptr) {
+    store_bf16x4(out + row * D + d, o);
+    return;
+  }
+  *reinterpret_cast<f32x4*>(sh.o_out + row * D + d) = o;
+  if (d == 0) sh.lse_out[row] = lse2 * kLn2;
+}
+
 // Row group g of a KV head: KT tiles of 16 rows, rows g*16*KT + t*16 + r16.  Loads the query
 // operands, clears the states and computes each lane's causal key limit per tile.
 template <int D, int KT>
@@ -771,9 +791,8 @@ void mx_paged_decode_splitkv(
     // Empty sequence: defined as a zero output.
     if (split == 0)
       for (int e = tid; e < nrows * (D / 4); e += 64 * NW)
-        store_bf16x4(out + (row_base(b, kv, sh) + row_offset(r0 + e / (D / 4), sh)) * D +
-                         4 * (e % (D / 4)),
-                     f32x4{0.f, 0.f, 0.f, 0.f});
+        store_row4<D>(out, sh, row_base(b, kv, sh) + row_offset(r0 + e / (D / 4), sh),
+                      4 * (e % (D / 4)), f32x4{0.f, 0.f, 0.f, 0.f}, -INFINITY);
     return;
   }
   const int t0 = split * sh.tokens_per_split;
@@ -803,7 +822,7 @@ void mx_paged_decode_splitkv(
     const f32x4 o = merged_head<D, NW, KT>(lds, hh, d, lse);
     const int64_t row = row_base(b, kv, sh) + row_offset(r0 + hh, sh);
     if (single) {
-      store_bf16x4(out + row * D + d, o);
+      store_row4<D>(out, sh, row, d, o, lse);
     } else if (sh.fused_combine) {  // read back by another workgroup of this launch
       store_partial4(part_o + (row * sh.num_splits + split) * D + d, o);
       if (d == 0) store_partial1(part_lse + row * sh.num_splits + split, lse);
@@ -864,7 +883,9 @@ void mx_paged_decode_splitkv(
         mx = bm;
       }
     }
-    store_bf16x4(out + row * D + d, acc * (wsum > 0.f ? 1.0f / wsum : 0.f));
+    const bool seen = wsum > 0.f;
+    store_row4<D>(out, sh, row, d, acc * (seen ? 1.0f / wsum : 0.f),
+                  seen ? mx + log2f(wsum) : -INFINITY);
   }
 }
 
@@ -923,9 +944,10 @@ void mx_paged_decode_balanced(
   // num_heads consecutive rows) are written by workgroup b % num_groups.
   for (int b = wg; b < B; b += sh.num_groups) {
     if (seq_lens[b] <= 0) {
-      uint16_t* ob = out + (int64_t)b * sh.seqlen_q * sh.num_heads * D;
+      const int64_t row0 = (int64_t)b * sh.seqlen_q * sh.num_heads;
       for (int e = tid; e < sh.seqlen_q * sh.num_heads * (D / 4); e += 64 * NW)
-        store_bf16x4(ob + 4 * (int64_t)e, f32x4{0.f, 0.f, 0.f, 0.f});
+        store_row4<D>(out, sh, row0 + e / (D / 4), 4 * (e % (D / 4)), f32x4{0.f, 0.f, 0.f, 0.f},
+                      -INFINITY);
     }
   }
 
@@ -1040,8 +1062,8 @@ void mx_paged_decode_balanced(
           const int hh = e / (D / 4);
           const int d = 4 * (e - hh * (D / 4));
           float lse;
-          store_bf16x4(out + (rbase + row_offset(r0 + hh, sh)) * D + d,
-                       merged_head<D, NW, KT>(lds, hh, d, lse));
+          const f32x4 o = merged_head<D, NW, KT>(lds, hh, d, lse);
+          store_row4<D>(out, sh, rbase + row_offset(r0 + hh, sh), d, o, lse);
         }
       } else {
         // Piece k of the unit goes to slot slot0 + k; level-l item j of the merge tree covers
@@ -1109,11 +1131,12 @@ void mx_paged_decode_balanced(
               acc += w * vals[t];
             }
             acc *= seen ? 1.0f / wsum : 0.f;
+            const float lse = seen ? mx + log2f(wsum) : -INFINITY;
             if (nnext == 1) {
-              store_bf16x4(out + (rbase + row_offset(r0 + hh, sh)) * D + d, acc);
+              store_row4<D>(out, sh, rbase + row_offset(r0 + hh, sh), d, acc, lse);
             } else {
               store_partial4(part_o + ((int64_t)gslot * TR + hh) * D + d, acc);
-              if (d == 0) s_lse[hh] = seen ? mx + log2f(wsum) : -INFINITY;
+              if (d == 0) s_lse[hh] = lse;
             }
           }
           if (nnext == 1) break;
@@ -1145,47 +1168,37 @@ void mx_paged_decode_balanced(
 }
 
 // ------------------------------------------------------------------------------------------
-// Combine kernel: out[row] = sum_s 2^(lse_s - M) * O_s / sum_s 2^(lse_s - M), M = max_s lse_s
-// over the splits that hold tokens of the row's sequence (optimized_c500_flash_attn.cu:666-728);
-// splits in which a causal row saw no key carry lse -inf (weight 0), and a row that saw none at
-// all is written as zeros.
+// LSE merge of partials: out[row] = sum_s 2^(lse_s - M) * O_s / sum_s 2^(lse_s - M), M = max_s
+// lse_s (optimized_c500_flash_attn.cu:666-728, log2 domain).  Partials with lse -inf (a causal
+// row that saw no key in that part) weigh 0, and a row no part saw a key for is zeros.
 // ------------------------------------------------------------------------------------------
 
+// One wave merges the n partials of one row: lane holds dims E*lane .. E*lane+E-1.  Partial s
+// sits at lse[s * lse_stride] (times lse_to_log2 in log2 units) and o[s * o_stride + E*lane ..].  One online pass, the loads of
+// kBatch partials issued together per round (the pass is latency-bound).  Returns the merged
+// log2-sum-exp (-inf when no part saw a key) and leaves the normalised dims in acc.
 template <int D>
-__global__ __launch_bounds__(64) void mx_paged_decode_combine(
-    const float* __restrict__ part_o, const float* __restrict__ part_lse,
-    const int32_t* __restrict__ seq_lens, uint16_t* __restrict__ out, int num_heads,
-    int seqlen_q, int num_splits, int tokens_per_split, int cap_tokens) {
-  constexpr int E = D / 64;  // output dims per lane
-  const int h = blockIdx.x;
-  const int bt = blockIdx.y;  // sequence * seqlen_q + query token
-  const int b = bt / seqlen_q;
-  const int lane = threadIdx.x;
-  int seq = min(seq_lens[b], cap_tokens);
-  if (seq <= tokens_per_split) return;  // single split (or empty): main kernel wrote it
-  const int nsv = (seq + tokens_per_split - 1) / tokens_per_split;
-  const int64_t row = (int64_t)bt * num_heads + h;
-  const float* lse = part_lse + row * num_splits;
-  const float* po = part_o + row * num_splits * D + E * lane;
-
-  // One online pass over the splits, the loads of kCombineBatch splits issued together per
-  // round (the pass is latency-bound: a row's partials are a few KB).
-  constexpr int kCombineBatch = 16;
+__device__ __forceinline__ float merge_row(float (&acc)[D / 64], const float* __restrict__ lse,
+                                           int64_t lse_stride, float lse_to_log2,
+                                           const float* __restrict__ o, int64_t o_stride, int n,
+                                           int lane) {
+  constexpr int E = D / 64;
+  constexpr int kBatch = 16;
+  const float* po = o + E * lane;
   float mx = -INFINITY;  // running max of the log2-sum-exps seen
-  float acc[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) acc[e] = 0.f;
   float wsum = 0.f;
-  for (int s0 = 0; s0 < nsv; s0 += kCombineBatch) {
-    float ls[kCombineBatch];
-    float vs[kCombineBatch][E];
-    // Every slot loads (past the last split it re-reads the last one), so the loads are
+  for (int s0 = 0; s0 < n; s0 += kBatch) {
+    float ls[kBatch];
+    float vs[kBatch][E];
+    // Every slot loads (past the last part it re-reads the last one), so the loads are
     // unconditional and issue back to back; the extra slots are masked by their lse below.
 #pragma unroll
-    for (int t = 0; t < kCombineBatch; ++t) {
-      const int sl = min(s0 + t, nsv - 1);
-      ls[t] = lse[sl];
-      const float* src = po + (int64_t)sl * D;
+    for (int t = 0; t < kBatch; ++t) {
+      const int64_t sl = min(s0 + t, n - 1);
+      ls[t] = lse[sl * lse_stride] * lse_to_log2;
+      const float* src = po + sl * o_stride;
       if constexpr (E == 1) {
         vs[t][0] = src[0];
       } else if constexpr (E == 2) {
@@ -1199,18 +1212,18 @@ __global__ __launch_bounds__(64) void mx_paged_decode_combine(
       }
     }
 #pragma unroll
-    for (int t = 0; t < kCombineBatch; ++t)
-      if (s0 + t >= nsv) ls[t] = -INFINITY;
+    for (int t = 0; t < kBatch; ++t)
+      if (s0 + t >= n) ls[t] = -INFINITY;
     float bm = mx;
 #pragma unroll
-    for (int t = 0; t < kCombineBatch; ++t) bm = fmaxf(bm, ls[t]);
-    if (bm > -INFINITY) {  // else: no split so far saw a key for this row
+    for (int t = 0; t < kBatch; ++t) bm = fmaxf(bm, ls[t]);
+    if (bm > -INFINITY) {  // else: no part so far saw a key for this row
       const float a = __builtin_amdgcn_exp2f(mx - bm);
       wsum *= a;
 #pragma unroll
       for (int e = 0; e < E; ++e) acc[e] *= a;
 #pragma unroll
-      for (int t = 0; t < kCombineBatch; ++t) {
+      for (int t = 0; t < kBatch; ++t) {
         const float w = __builtin_amdgcn_exp2f(ls[t] - bm);
         wsum += w;
 #pragma unroll
@@ -1219,18 +1232,73 @@ __global__ __launch_bounds__(64) void mx_paged_decode_combine(
       mx = bm;
     }
   }
-  if (!(wsum > 0.f)) wsum = 1.f;  // a row no split saw a key for: zeros
-  const float inv = 1.0f / wsum;
+  const bool seen = wsum > 0.f;
+  const float inv = seen ? 1.0f / wsum : 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) acc[e] *= inv;
+  return seen ? mx + log2f(wsum) : -INFINITY;
+}
+
+// Writes a merged row (log2-sum-exp lse): bf16 to out, or (partial outputs) fp32 to o_out and
+// the natural-log sum-exp to lse_out.
+template <int D>
+__device__ __forceinline__ void store_merged_row(const float (&acc)[D / 64], float lse,
+                                                 uint16_t* __restrict__ out,
+                                                 float* __restrict__ o_out,
+                                                 float* __restrict__ lse_out, int64_t row,
+                                                 int lane) {
+  constexpr int E = D / 64;
+  if (o_out != nullptr) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) o_out[row * D + E * lane + e] = acc[e];
+    if (lane == 0) lse_out[row] = lse * kLn2;
+    return;
+  }
   uint16_t* op = out + row * D + E * lane;
   if constexpr (E == 1) {
-    op[0] = __builtin_bit_cast(uint16_t, (__bf16)(acc[0] * inv));
+    op[0] = __builtin_bit_cast(uint16_t, (__bf16)acc[0]);
   } else if constexpr (E == 2) {
-    *reinterpret_cast<uint32_t*>(op) = pack_bf16x2(acc[0] * inv, acc[1] * inv);
+    *reinterpret_cast<uint32_t*>(op) = pack_bf16x2(acc[0], acc[1]);
   } else {
-    const u32x2 w = {pack_bf16x2(acc[0] * inv, acc[1] * inv),
-                     pack_bf16x2(acc[2] * inv, acc[3] * inv)};
+    const u32x2 w = {pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
     *reinterpret_cast<u32x2*>(op) = w;
   }
+}
+
+// Second launch of the split grid: one wave per (query head, sequence * query token) merges the
+// splits that hold tokens of the row's sequence.
+template <int D>
+__global__ __launch_bounds__(64) void mx_paged_decode_combine(
+    const float* __restrict__ part_o, const float* __restrict__ part_lse,
+    const int32_t* __restrict__ seq_lens, uint16_t* __restrict__ out, float* __restrict__ o_out,
+    float* __restrict__ lse_out, int num_heads, int seqlen_q, int num_splits,
+    int tokens_per_split, int cap_tokens) {
+  const int h = blockIdx.x;
+  const int bt = blockIdx.y;  // sequence * seqlen_q + query token
+  const int b = bt / seqlen_q;
+  const int lane = threadIdx.x;
+  const int seq = min(seq_lens[b], cap_tokens);
+  if (seq <= tokens_per_split) return;  // single split (or empty): main kernel wrote it
+  const int nsv = (seq + tokens_per_split - 1) / tokens_per_split;
+  const int64_t row = (int64_t)bt * num_heads + h;
+  float acc[D / 64];
+  const float lse = merge_row<D>(acc, part_lse + row * num_splits, 1, 1.0f,
+                                 part_o + row * num_splits * D, D, nsv, lane);
+  store_merged_row<D>(acc, lse, out, o_out, lse_out, row, lane);
+}
+
+// mx_lse_merge: rows merged over `parts` gathered partials, part-major ([parts, rows, D] and
+// [parts, rows], natural-log sum-exps); one wave per row.
+template <int D>
+__global__ __launch_bounds__(64) void mx_lse_merge_kernel(const float* __restrict__ o_parts,
+                                                          const float* __restrict__ lse_parts,
+                                                          int64_t rows, int parts,
+                                                          uint16_t* __restrict__ out) {
+  const int64_t row = blockIdx.x;
+  float acc[D / 64];
+  const float lse = merge_row<D>(acc, lse_parts + row, rows, kLog2e, o_parts + row * D,
+                                 rows * D, parts, threadIdx.x);
+  store_merged_row<D>(acc, lse, out, nullptr, nullptr, row, threadIdx.x);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1309,6 +1377,7 @@ constexpr int64_t kMaxTokensPerSplit = 16384;  // bounds one workgroup's share o
 constexpr int64_t kMaxGridDim = 65535;
 constexpr int64_t kBalancedMinUnits = 64;
 constexpr int64_t kFusedMaxSplits = 16;  // split grid: merge in-kernel up to this many splits
+constexpr int64_t kMaxMergeRows = int64_t(1) << 25;  // mx_lse_merge: 64 * rows work-items < 2^31
 
 int64_t groups_per_cu(int64_t head_dim) { return head_dim == 64 ? 2 : 1; }
 
@@ -1524,7 +1593,7 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
                   const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
                   int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads, int64_t page_size,
                   int64_t num_pages, int64_t max_pages, float scale, char* ws, int32_t phase,
-                  hipStream_t stream) {
+                  float* o_out, float* lse_out, hipStream_t stream) {
   constexpr int kNW = waves_per_group<D>();
   constexpr int kNBUF = ring_depth<D>();
   MainShape sh;
@@ -1551,6 +1620,8 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   sh.num_groups = (int)plan.groups;
   sh.unit_overhead = MX_UNIT_OVERHEAD;
   sh.num_slots = (int)plan.slots;
+  sh.o_out = o_out;
+  sh.lse_out = lse_out;
   uint32_t* status = reinterpret_cast<uint32_t*>(ws);
 
   if (plan.schedule == MX_SCHEDULE_BALANCED) {
@@ -1591,8 +1662,9 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   if (phase != MX_PHASE_MAIN_ONLY && plan.splits > 1 && !fused) {
     const dim3 grid((unsigned)num_heads, (unsigned)(batch * seqlen_q));
     hipLaunchKernelGGL(mx_paged_decode_combine<D>, grid, dim3(64), 0, stream, part_o, part_lse,
-                       seq_lens, static_cast<uint16_t*>(out), (int)num_heads, (int)seqlen_q,
-                       (int)plan.splits, (int)plan.tokens_per_split, (int)plan.cap_tokens);
+                       seq_lens, static_cast<uint16_t*>(out), o_out, lse_out, (int)num_heads,
+                       (int)seqlen_q, (int)plan.splits, (int)plan.tokens_per_split,
+                       (int)plan.cap_tokens);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -1640,16 +1712,18 @@ int64_t mx_paged_gqa_decode_workspace_size(int64_t batch, int64_t seqlen_q, int6
   return plan.workspace_bytes;
 }
 
-int mx_paged_gqa_decode(const void* q, const void* k_cache, const void* v_cache, void* out,
-                        const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
-                        int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads,
-                        int64_t head_dim, int64_t page_size, int64_t num_pages,
-                        int64_t max_pages_per_seq, int64_t max_seq_len, int32_t causal,
-                        float scale, int64_t num_splits, void* workspace, int64_t workspace_bytes,
-                        int32_t phase, void* stream) {
-  if (!q || !k_cache || !v_cache || !out || !seq_lens || !block_table)
-    return fail(MX_STATUS_NULL_POINTER,
-                "q, k_cache, v_cache, out, seq_lens and block_table must be non-NULL");
+}  // extern "C"
+
+namespace {
+
+// Shared by mx_paged_gqa_decode (bf16 into out) and mx_paged_gqa_decode_partial (fp32 rows into
+// o_out and natural-log sum-exps into lse_out; out is then null).
+int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* out, float* o_out,
+                float* lse_out, const int32_t* seq_lens, const int32_t* block_table,
+                int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads,
+                int64_t head_dim, int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
+                int64_t max_seq_len, int32_t causal, float scale, int64_t num_splits,
+                void* workspace, int64_t workspace_bytes, int32_t phase, void* stream) {
   if (phase != 0 && phase != MX_PHASE_MAIN_ONLY && phase != MX_PHASE_COMBINE_ONLY)
     return fail(MX_STATUS_INVALID_ARGUMENT, "phase must be 0, 1 or 2");
   if (causal != 0 && causal != 1) return fail(MX_STATUS_INVALID_ARGUMENT, "causal must be 0 or 1");
@@ -1676,7 +1750,7 @@ int mx_paged_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
 #define MX_LAUNCH(DIM, CAUSAL, KT)                                                            \
   launch<DIM, CAUSAL, KT>(plan, q, k_cache, v_cache, out, seq_lens, block_table, batch, seqlen_q, \
                       num_heads, num_kv_heads, page_size, num_pages, max_pages_per_seq, scale, \
-                      ws, phase, s)
+                      ws, phase, o_out, lse_out, s)
   const bool pair = plan.tiles_per_group == 2;
   switch (head_dim) {
     case 64:
@@ -1692,6 +1766,87 @@ int mx_paged_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
       break;
   }
 #undef MX_LAUNCH
+  if (e != hipSuccess)
+    return fail(MX_STATUS_HIP_ERROR, std::string("kernel launch failed: ") + hipGetErrorString(e));
+  return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int mx_paged_gqa_decode(const void* q, const void* k_cache, const void* v_cache, void* out,
+                        const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
+                        int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads,
+                        int64_t head_dim, int64_t page_size, int64_t num_pages,
+                        int64_t max_pages_per_seq, int64_t max_seq_len, int32_t causal,
+                        float scale, int64_t num_splits, void* workspace, int64_t workspace_bytes,
+                        int32_t phase, void* stream) {
+  if (!q || !k_cache || !v_cache || !out || !seq_lens || !block_table)
+    return fail(MX_STATUS_NULL_POINTER,
+                "q, k_cache, v_cache, out, seq_lens and block_table must be non-NULL");
+  return decode_impl(q, k_cache, v_cache, out, nullptr, nullptr, seq_lens, block_table, batch,
+                     seqlen_q, num_heads, num_kv_heads, head_dim, page_size, num_pages,
+                     max_pages_per_seq, max_seq_len, causal, scale, num_splits, workspace,
+                     workspace_bytes, phase, stream);
+}
+
+int mx_paged_gqa_decode_partial(const void* q, const void* k_cache, const void* v_cache,
+                                float* o_partial, float* lse_partial, const int32_t* seq_lens,
+                                const int32_t* block_table, int64_t batch, int64_t seqlen_q,
+                                int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                                int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
+                                int64_t max_seq_len, int32_t causal, float scale,
+                                int64_t num_splits, void* workspace, int64_t workspace_bytes,
+                                void* stream) {
+  if (!q || !k_cache || !v_cache || !o_partial || !lse_partial || !seq_lens || !block_table)
+    return fail(MX_STATUS_NULL_POINTER,
+                "q, k_cache, v_cache, o_partial, lse_partial, seq_lens and block_table must be "
+                "non-NULL");
+  if (reinterpret_cast<uintptr_t>(o_partial) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(lse_partial) % 4 != 0)
+    return fail(MX_STATUS_INVALID_ARGUMENT,
+                "o_partial must be 16-byte aligned and lse_partial 4-byte aligned");
+  return decode_impl(q, k_cache, v_cache, nullptr, o_partial, lse_partial, seq_lens,
+                     block_table, batch, seqlen_q, num_heads, num_kv_heads, head_dim, page_size,
+                     num_pages, max_pages_per_seq, max_seq_len, causal, scale, num_splits,
+                     workspace, workspace_bytes, 0, stream);
+}
+
+int mx_lse_merge(const float* o_parts, const float* lse_parts, int64_t num_parts, int64_t rows,
+                 int64_t head_dim, void* out, void* stream) {
+  if (!o_parts || !lse_parts || !out)
+    return fail(MX_STATUS_NULL_POINTER, "o_parts, lse_parts and out must be non-NULL");
+  if (num_parts < 1 || rows < 0)
+    return fail(MX_STATUS_INVALID_SHAPE, "num_parts must be >= 1 and rows >= 0");
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(MX_STATUS_UNSUPPORTED, "head_dim must be 64, 128 or 256");
+  if (reinterpret_cast<uintptr_t>(o_parts) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(lse_parts) % 4 != 0 ||
+      reinterpret_cast<uintptr_t>(out) % 8 != 0)
+    return fail(MX_STATUS_INVALID_ARGUMENT,
+                "o_parts must be 16-byte, lse_parts 4-byte and out 8-byte aligned");
+  if (rows > kMaxMergeRows || num_parts > INT32_MAX)
+    return fail(MX_STATUS_UNSUPPORTED, "rows must be <= 2^25 and num_parts < 2^31");
+  if (rows == 0) return ok();
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)rows);
+  uint16_t* o = static_cast<uint16_t*>(out);
+  switch (head_dim) {
+    case 64:
+      hipLaunchKernelGGL(mx_lse_merge_kernel<64>, grid, dim3(64), 0, s, o_parts, lse_parts, rows,
+                         (int)num_parts, o);
+      break;
+    case 128:
+      hipLaunchKernelGGL(mx_lse_merge_kernel<128>, grid, dim3(64), 0, s, o_parts, lse_parts,
+                         rows, (int)num_parts, o);
+      break;
+    default:
+      hipLaunchKernelGGL(mx_lse_merge_kernel<256>, grid, dim3(64), 0, s, o_parts, lse_parts,
+                         rows, (int)num_parts, o);
+      break;
+  }
+  const hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return fail(MX_STATUS_HIP_ERROR, std::string("kernel launch failed: ") + hipGetErrorString(e));
   return ok();

@@ -17,6 +17,10 @@ import torch
 from . import _lib
 
 
+FUSED_MAX_SPLITS = 16      # kFusedMaxSplits in csrc/paged_decode.hip
+COUNTER_SLOTS = 4096 + 8192  # kMaxSlots in csrc/paged_decode.hip
+
+
 def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
     return ctypes.c_void_p(0 if t is None else t.data_ptr())
 
@@ -37,9 +41,9 @@ def plan(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, page_size
          num_cus: int = 0, seqlen_q: int = 1) -> dict:
     """Split plan of a call (host only when ``num_cus`` > 0).
 
-    Returns ``{"schedule", "splits", "tokens_per_split", "workgroups", "workspace_bytes"}``
-    (schedule: "split_grid" or "balanced"); raises MXAttnError for an invalid or unsupported
-    shape.
+    Returns ``{"schedule", "splits", "tokens_per_split", "workgroups", "workspace_bytes",
+    "launches"}`` (schedule: "split_grid" or "balanced"; launches: kernels a phase-0 call runs);
+    raises MXAttnError for an invalid or unsupported shape.
     """
     lib = _lib.load()
     sch, ns, tps, wgs, ws = (ctypes.c_int64() for _ in range(5))
@@ -49,9 +53,19 @@ def plan(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, page_size
                                       ctypes.byref(sch), ctypes.byref(ns), ctypes.byref(tps),
                                       ctypes.byref(wgs), ctypes.byref(ws))
     _lib.check(st)
-    return {"schedule": "balanced" if sch.value == _lib.MX_SCHEDULE_BALANCED else "split_grid",
-            "splits": ns.value, "tokens_per_split": tps.value, "workgroups": wgs.value,
-            "workspace_bytes": ws.value}
+    schedule = "balanced" if sch.value == _lib.MX_SCHEDULE_BALANCED else "split_grid"
+    # Launches of a phase-0 call: the balanced schedule and the split grid with one split are
+    # one launch; the split grid merges in-kernel up to FUSED_MAX_SPLITS splits when its units'
+    # arrival counters fit, else a combine kernel follows (csrc/paged_decode.hip,
+    # kFusedMaxSplits and kMaxSlots).
+    G = num_heads // num_kv_heads
+    rows = seqlen_q * G
+    per_group = 32 if rows > 16 and head_dim <= 128 else 16
+    units = batch * num_kv_heads * -(-rows // per_group)
+    two = (schedule == "split_grid" and ns.value > 1 and
+           (ns.value > FUSED_MAX_SPLITS or units > COUNTER_SLOTS))
+    return {"schedule": schedule, "splits": ns.value, "tokens_per_split": tps.value,
+            "workgroups": wgs.value, "workspace_bytes": ws.value, "launches": 2 if two else 1}
 
 
 def workspace_size(batch: int, num_heads: int, num_kv_heads: int, head_dim: int,
@@ -78,20 +92,8 @@ def _query_shape(q: torch.Tensor) -> tuple[int, int, int, int]:
     return tuple(q.shape)
 
 
-def paged_gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
-                     block_table: torch.Tensor, seq_lens: torch.Tensor,
-                     scale: float | None = None, *, out: torch.Tensor | None = None,
-                     causal: bool = False, num_splits: int = 0, max_seq_len: int = 0,
-                     workspace: torch.Tensor | None = None, phase: int = 0,
-                     stream=None) -> torch.Tensor:
-    """out[b, i, h] = softmax(q[b, i, h] . K_b^T * scale) . V_b over the first seq_lens[b]
-    tokens (with ``causal``, query token i of seqlen_q sees keys t < L - seqlen_q + i + 1).
-
-    q: [B, Hq, D] (one query token) or [B, seqlen_q, Hq, D] bf16; k_cache / v_cache:
-    [num_pages, page_size, Hkv, D] bf16; block_table: [B, max_pages] int32; seq_lens: [B] int32;
-    all on one GPU, contiguous.  ``scale`` defaults to 1/sqrt(D) (reference
-    submission_clean.cu:451).
-    """
+def _check_decode_inputs(q, k_cache, v_cache, block_table, seq_lens):
+    """Validates the decode operands; returns (device, B, SQ, Hq, D, num_pages, P, Hkv)."""
     _require(q.is_cuda, "q must be a device tensor")
     dev = q.device
     for name, t, dt in (("q", q, torch.bfloat16), ("k_cache", k_cache, torch.bfloat16),
@@ -109,6 +111,33 @@ def paged_gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     _require(block_table.dim() == 2 and block_table.shape[0] == B,
              "block_table must be [B, max_pages]")
     _require(seq_lens.shape == (B,), "seq_lens must be [B]")
+    return dev, B, SQ, Hq, D, num_pages, P, Hkv
+
+
+def _workspace_bytes(workspace, dev) -> int:
+    if workspace is None:
+        return 0
+    _require(workspace.is_cuda and workspace.device == dev and workspace.is_contiguous(),
+             "workspace must be a contiguous tensor on the same device")
+    return workspace.numel() * workspace.element_size()
+
+
+def paged_gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                     block_table: torch.Tensor, seq_lens: torch.Tensor,
+                     scale: float | None = None, *, out: torch.Tensor | None = None,
+                     causal: bool = False, num_splits: int = 0, max_seq_len: int = 0,
+                     workspace: torch.Tensor | None = None, phase: int = 0,
+                     stream=None) -> torch.Tensor:
+    """out[b, i, h] = softmax(q[b, i, h] . K_b^T * scale) . V_b over the first seq_lens[b]
+    tokens (with ``causal``, query token i of seqlen_q sees keys t < L - seqlen_q + i + 1).
+
+    q: [B, Hq, D] (one query token) or [B, seqlen_q, Hq, D] bf16; k_cache / v_cache:
+    [num_pages, page_size, Hkv, D] bf16; block_table: [B, max_pages] int32; seq_lens: [B] int32;
+    all on one GPU, contiguous.  ``scale`` defaults to 1/sqrt(D) (reference
+    submission_clean.cu:451).
+    """
+    dev, B, SQ, Hq, D, num_pages, P, Hkv = _check_decode_inputs(q, k_cache, v_cache,
+                                                                block_table, seq_lens)
     if out is None:
         out = torch.empty_like(q)
     else:
@@ -116,11 +145,7 @@ def paged_gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
                  and out.device == dev, "out must be a contiguous bf16 tensor shaped like q")
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    ws_bytes = 0
-    if workspace is not None:
-        _require(workspace.is_cuda and workspace.device == dev and workspace.is_contiguous(),
-                 "workspace must be a contiguous tensor on the same device")
-        ws_bytes = workspace.numel() * workspace.element_size()
+    ws_bytes = _workspace_bytes(workspace, dev)
     lib = _lib.load()
     with torch.cuda.device(dev):
         st = lib.mx_paged_gqa_decode(
@@ -128,6 +153,71 @@ def paged_gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
             _ptr(block_table), B, SQ, Hq, Hkv, D, P, num_pages, block_table.shape[1],
             max_seq_len, int(bool(causal)), float(scale), num_splits, _ptr(workspace), ws_bytes,
             phase, _stream_handle(stream, dev))
+    _lib.check(st)
+    return out
+
+
+def paged_gqa_decode_partial(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                             block_table: torch.Tensor, seq_lens: torch.Tensor,
+                             scale: float | None = None, *, causal: bool = False,
+                             num_splits: int = 0, max_seq_len: int = 0,
+                             workspace: torch.Tensor | None = None,
+                             stream=None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Decode over one shard of the keys, kept unmerged for a cross-shard merge.
+
+    Same operands as ``paged_gqa_decode`` with ``block_table`` / ``seq_lens`` describing this
+    shard's keys.  Returns ``(o, lse)``: o fp32 shaped like q (each row's attention output over
+    the shard's keys) and lse fp32 of q's shape without D (natural-log sum of
+    exp(scale * q . k) over them); a row that sees no key has o = 0, lse = -inf.  The split
+    phase of optimized_c500_flash_attn.cu:537-551 for a caller-chosen key range; merge the
+    shards' results with ``lse_merge``.
+    """
+    dev, B, SQ, Hq, D, num_pages, P, Hkv = _check_decode_inputs(q, k_cache, v_cache,
+                                                                block_table, seq_lens)
+    o = torch.empty(q.shape, dtype=torch.float32, device=dev)
+    lse = torch.empty(q.shape[:-1], dtype=torch.float32, device=dev)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    ws_bytes = _workspace_bytes(workspace, dev)
+    with torch.cuda.device(dev):
+        st = _lib.load().mx_paged_gqa_decode_partial(
+            _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(o), _ptr(lse), _ptr(seq_lens),
+            _ptr(block_table), B, SQ, Hq, Hkv, D, P, num_pages, block_table.shape[1],
+            max_seq_len, int(bool(causal)), float(scale), num_splits, _ptr(workspace), ws_bytes,
+            _stream_handle(stream, dev))
+    _lib.check(st)
+    return o, lse
+
+
+def lse_merge(o_parts: torch.Tensor, lse_parts: torch.Tensor, *,
+              out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Merges partials of the same rows (combine_splits, optimized_c500_flash_attn.cu:666-728).
+
+    o_parts: [parts, ..., D] fp32 and lse_parts: [parts, ...] fp32 (natural log), e.g. the
+    stacked ``paged_gqa_decode_partial`` results of every shard.  Returns bf16 [..., D]:
+    sum_p exp(lse_p - M) o_p / sum_p exp(lse_p - M) with M = max_p lse_p; rows no part saw a
+    key for are zeros.
+    """
+    _require(o_parts.is_cuda, "o_parts must be a device tensor")
+    dev = o_parts.device
+    for name, t in (("o_parts", o_parts), ("lse_parts", lse_parts)):
+        _require(t.device == dev, f"{name} must be on {dev}")
+        _require(t.dtype == torch.float32, f"{name} must be float32, got {t.dtype}")
+        _require(t.is_contiguous(), f"{name} must be contiguous")
+    _require(o_parts.dim() >= 2 and tuple(lse_parts.shape) == tuple(o_parts.shape[:-1]),
+             "o_parts must be [parts, ..., D] and lse_parts [parts, ...]")
+    parts, D = o_parts.shape[0], o_parts.shape[-1]
+    rows = o_parts[0].numel() // D if parts > 0 else 0
+    shape = tuple(o_parts.shape[1:])
+    if out is None:
+        out = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+    else:
+        _require(tuple(out.shape) == shape and out.dtype == torch.bfloat16 and
+                 out.is_contiguous() and out.device == dev,
+                 "out must be a contiguous bf16 tensor shaped like o_parts[0]")
+    with torch.cuda.device(dev):
+        st = _lib.load().mx_lse_merge(_ptr(o_parts), _ptr(lse_parts), parts, rows, D, _ptr(out),
+                                      _stream_handle(stream, dev))
     _lib.check(st)
     return out
 

@@ -17,6 +17,12 @@ Pinning (what each function is checked against, in tests/test_oracle.py):
                           the split-KV + log-sum-exp merge (optimized_c500_flash_attn.cu:537-551,
                           666-728); pinned by equality with the unsplit oracle for every split
                           size.
+  paged_decode_partial_reference / lse_merge_reference
+                          one shard's unmerged (o, lse) and the merge of gathered shards
+                          (optimized_c500_flash_attn.cu:537-551, 666-728); lse pinned by
+                          scipy.special.logsumexp and the closed form log(L) (zero keys), the
+                          merge of any page sharding pinned by equality with the unsharded
+                          decode (itself pinned by SDPA), including causal multi-token shards.
   paged_kv_append_reference
                           the paged K/V append (flash_attn_with_kvcache's k / v); pinned by
                           the round trip through the decode oracle against plain attention
@@ -29,7 +35,9 @@ unpinned; the task.md:85-96 example is kept as a shape fixture under tests/golde
 from .paged_attention import (  # noqa: F401
     combine_partials,
     kv_bytes,
+    lse_merge_reference,
     paged_decode_fp64,
+    paged_decode_partial_reference,
     paged_decode_reference,
     paged_kv_append_reference,
     split_partials,

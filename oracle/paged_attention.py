@@ -28,7 +28,7 @@ def _as3(q: torch.Tensor) -> torch.Tensor:
 
 
 def kv_bytes(seq_lens, num_kv_heads: int, head_dim: int) -> int:
-    """Algorithmic K+V bytes of one call (BASELINE.md byte formula)."""
+    """Algorithmic K+V bytes of one call: sum_b L_b * Hkv * D * 2 (K and V) * 2 bytes."""
     total = int(torch.as_tensor(seq_lens).to(torch.int64).clamp(min=0).sum().item())
     return total * num_kv_heads * head_dim * 2 * 2
 
@@ -212,3 +212,58 @@ def paged_kv_append_reference(k_new, v_new, k_cache, v_cache, block_table, seq_l
             v_out[pid, pos % P] = vn[b, j]
     return k_out, v_out, flags
 
+
+
+def paged_decode_partial_reference(q, k_cache, v_cache, block_table, seq_lens, scale=None,
+                                   causal: bool = False):
+    """One shard's unmerged decode (the split phase of optimized_c500_flash_attn.cu:537-551 for
+    a caller-chosen key range), fp64 on CPU.
+
+    ``block_table`` / ``seq_lens`` describe the shard's keys.  Returns (o, lse): o of q's shape,
+    each row's softmax-weighted V over the shard's visible keys; lse of q's shape without D,
+    log(sum_t exp(scale * q . k_t)) over them (natural log).  With ``causal`` the end-aligned
+    mask is taken on the shard's own length.  Rows that see no key: o = 0, lse = -inf.
+    """
+    q4 = q if q.dim() == 4 else q.unsqueeze(1)
+    B, SQ, Hq, D = q4.shape
+    Hkv = k_cache.shape[2]
+    G = Hq // Hkv
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    lens = torch.as_tensor(seq_lens).cpu()
+    o = torch.zeros(B, SQ, Hq, D, dtype=torch.float64)
+    lse = torch.full((B, SQ, Hq), float("-inf"), dtype=torch.float64)
+    for b in range(B):
+        L = int(lens[b])
+        if L <= 0:
+            continue
+        k, v = _gather_sequence(k_cache, v_cache, block_table, b, L)
+        kt = k.double().permute(1, 2, 0)                                # [Hkv, D, L]
+        vt = v.double().permute(1, 0, 2)                                # [Hkv, L, D]
+        qb = q4[b].double().view(SQ, Hkv, G, D).permute(1, 0, 2, 3).reshape(Hkv, SQ * G, D)
+        logits = torch.matmul(qb, kt) * scale                          # [Hkv, SQ*G, L]
+        vis = torch.from_numpy(np.repeat(_visible(L, SQ, causal), G, axis=0))
+        logits = logits.masked_fill(~vis, float("-inf"))
+        lse_b = torch.logsumexp(logits, dim=-1)                        # -inf: no visible key
+        attn = torch.exp(logits - lse_b.unsqueeze(-1)).nan_to_num(0.0)
+        ob = torch.matmul(attn, vt)                                    # [Hkv, SQ*G, D]
+        o[b] = ob.view(Hkv, SQ, G, D).permute(1, 0, 2, 3).reshape(SQ, Hq, D)
+        lse[b] = lse_b.view(Hkv, SQ, G).permute(1, 0, 2).reshape(SQ, Hq)
+    if q.dim() == 3:
+        return o[:, 0], lse[:, 0]
+    return o, lse
+
+
+def lse_merge_reference(o_parts, lse_parts) -> np.ndarray:
+    """Log-sum-exp merge of gathered partials (combine_splits, optimized_c500_flash_attn.cu:
+    666-728), fp64: o_parts [parts, ..., D], lse_parts [parts, ...] (natural log).  With
+    M = max_p lse_p: out = sum_p e^(lse_p - M) o_p / sum_p e^(lse_p - M); rows whose every lse is
+    -inf are zeros."""
+    o = np.asarray(o_parts, dtype=np.float64)
+    ls = np.asarray(lse_parts, dtype=np.float64)
+    m = ls.max(axis=0)
+    seen = np.isfinite(m)
+    w = np.exp(ls - np.where(seen, m, 0.0)[None])                      # 0 for -inf parts
+    num = (w[..., None] * o).sum(0)
+    den = w.sum(0)
+    return np.where(seen[..., None], num / np.where(seen, den, 1.0)[..., None], 0.0)

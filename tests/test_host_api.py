@@ -283,3 +283,87 @@ def test_append_rejects_invalid_arguments(over, status):
 
 def test_append_of_zero_tokens_is_a_no_op():
     assert _append(S=0) == _lib.MX_STATUS_OK
+
+
+def test_python_launch_count_mirrors_the_library_constants():
+    """decode.plan()'s "launches" mirrors kFusedMaxSplits / kMaxSlots of the kernel source."""
+    import re
+    from mx_flash_attn_kernel_opt__amd import decode
+    src = open(os.path.join(REPO, "mx_flash_attn_kernel_opt__amd", "csrc",
+                            "paged_decode.hip")).read()
+    assert int(re.search(r"kFusedMaxSplits = (\d+);", src).group(1)) == decode.FUSED_MAX_SPLITS
+    m = re.search(r"kMaxSlots = (\d+) \+ (\d+);", src)
+    assert int(m.group(1)) + int(m.group(2)) == decode.COUNTER_SLOTS
+    assert plan(4, 32, 8, 128, 16, 64, 0, 4, num_cus=256)["launches"] == 1
+    assert plan(4, 32, 8, 128, 16, 64, 0, 32, num_cus=256)["launches"] == 2
+    assert plan(64, 32, 8, 128, 16, 64, 0, 0, num_cus=256)["launches"] == 1   # balanced
+
+
+# ------------------------------------------------------------------------------------------
+# Sharded-decode entry points: validation (no HIP call is reached on these paths)
+# ------------------------------------------------------------------------------------------
+
+def _partial(**over):
+    args = dict(q=FAKE, k=FAKE, v=FAKE, o=FAKE, lse=FAKE, lens=FAKE, table=FAKE, B=2, SQ=1,
+                Hq=32, Hkv=8, D=128, P=16, pages=64, max_pages=32, max_seq=0, causal=0,
+                scale=0.088, ns=2, ws=FAKE, ws_bytes=1 << 30, stream=None)
+    args.update(over)
+    a = args
+    return _lib.load().mx_paged_gqa_decode_partial(
+        a["q"], a["k"], a["v"], a["o"], a["lse"], a["lens"], a["table"], a["B"], a["SQ"],
+        a["Hq"], a["Hkv"], a["D"], a["P"], a["pages"], a["max_pages"], a["max_seq"], a["causal"],
+        a["scale"], a["ns"], a["ws"], a["ws_bytes"], a["stream"])
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(o=None), _lib.MX_STATUS_NULL_POINTER),
+    (dict(lse=None), _lib.MX_STATUS_NULL_POINTER),
+    (dict(table=None), _lib.MX_STATUS_NULL_POINTER),
+    (dict(o=ctypes.c_void_p(0x1008)), _lib.MX_STATUS_INVALID_ARGUMENT),   # not 16-byte aligned
+    (dict(lse=ctypes.c_void_p(0x1002)), _lib.MX_STATUS_INVALID_ARGUMENT),
+    (dict(Hq=30, Hkv=8), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(D=96), _lib.MX_STATUS_UNSUPPORTED),
+    (dict(causal=2), _lib.MX_STATUS_INVALID_ARGUMENT),
+    (dict(scale=float("nan")), _lib.MX_STATUS_INVALID_ARGUMENT),
+    (dict(ws_bytes=100), _lib.MX_STATUS_WORKSPACE_TOO_SMALL),
+])
+def test_partial_decode_rejects_invalid_arguments(over, status):
+    assert _partial(**over) == status
+    assert _lib.load().mx_last_error()
+
+
+def _merge(o=FAKE, lse=FAKE, parts=4, rows=10, D=128, out=FAKE):
+    return _lib.load().mx_lse_merge(o, lse, parts, rows, D, out, None)
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(o=None), _lib.MX_STATUS_NULL_POINTER),
+    (dict(lse=None), _lib.MX_STATUS_NULL_POINTER),
+    (dict(out=None), _lib.MX_STATUS_NULL_POINTER),
+    (dict(parts=0), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(rows=-1), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(D=96), _lib.MX_STATUS_UNSUPPORTED),
+    (dict(o=ctypes.c_void_p(0x1008)), _lib.MX_STATUS_INVALID_ARGUMENT),
+    (dict(out=ctypes.c_void_p(0x1004)), _lib.MX_STATUS_INVALID_ARGUMENT),
+    (dict(rows=(1 << 25) + 1), _lib.MX_STATUS_UNSUPPORTED),
+])
+def test_lse_merge_rejects_invalid_arguments(over, status):
+    assert _merge(**over) == status
+    assert _lib.load().mx_last_error()
+
+
+def test_lse_merge_of_zero_rows_is_a_no_op():
+    assert _merge(rows=0) == _lib.MX_STATUS_OK
+
+
+def test_shard_pages_rejects_bad_arguments():
+    import torch
+    from mx_flash_attn_kernel_opt__amd import shard_pages
+    table = torch.zeros(2, 4, dtype=torch.int32)
+    lens = torch.tensor([5, 9], dtype=torch.int32)
+    with pytest.raises(ValueError):
+        shard_pages(table, lens, 16, 0)
+    with pytest.raises(ValueError):
+        shard_pages(table, lens, 16, 2, seqlen_q=0)
+    with pytest.raises(ValueError):
+        shard_pages(table, lens[:1], 16, 2)
