@@ -24,8 +24,8 @@
  * Supported shapes: head_dim in {64, 128, 256}; page_size in {16, 32, 64, 128, 256};
  * num_heads % num_kv_heads == 0 and num_heads / num_kv_heads <= 16; seqlen_q >= 1 with
  * batch * seqlen_q <= 65535; causal 0 or 1.  The seqlen_q * (num_heads / num_kv_heads) query
- * rows of one KV head are processed 16 at a time: every further 16 rows stream that head's
- * K/V once more.
+ * rows of one KV head are processed in groups of 16 rows (32 when there are more than 16 and
+ * head_dim <= 128): every further group streams that head's K/V once more.
  *
  * Every call is asynchronous on the given stream (NULL = the legacy default stream) and never
  * synchronises.  Calls that share one workspace (including the library's internal one) must
@@ -55,8 +55,9 @@ extern "C" {
 #define MX_DEVICE_SEQ_TOO_LONG 2u   /* seq_lens[b] exceeded the capacity the call was planned for */
 
 /* Schedules reported by mx_paged_gqa_decode_plan. */
-#define MX_SCHEDULE_SPLIT_GRID 0   /* grid (Hkv * row tiles, batch, splits) + combine kernel
-                                      when splits > 1                                             */
+#define MX_SCHEDULE_SPLIT_GRID 0   /* grid (Hkv * row groups, batch, splits); with 2-16 splits
+                                      the last split of each unit merges, above 16 a combine
+                                      kernel follows                                              */
 #define MX_SCHEDULE_BALANCED 1     /* one launch of a fixed number of workgroups that divide the
                                       batch's K/V chunks evenly from seq_lens on the device and
                                       merge split sequences themselves                            */
@@ -99,10 +100,12 @@ void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_pa
  *                      splits, at most max_pages_per_seq*page_size) are clamped and flagged
  *                      (MX_DEVICE_SEQ_TOO_LONG).
  *   causal             0, or 1 for the end-aligned causal mask of multi-token queries.
- *   num_splits         0 = automatic: the balanced schedule when batch <= 512 and
- *                      64 <= units <= 8192 (units = batch * num_kv_heads *
- *                      ceil(seqlen_q * num_heads / num_kv_heads / 16)), else the split grid
- *                      with a CU-count-driven split count;
+ *   num_splits         0 = automatic: the balanced schedule when batch <= 512,
+ *                      64 <= units <= 8192 (units = batch * num_kv_heads * query row
+ *                      groups; a row group is 16 rows, or 32 when seqlen_q * num_heads /
+ *                      num_kv_heads > 16 and head_dim <= 128) and the capacity is at least
+ *                      2048 tokens (1024 with 512+ units); else the split grid with a
+ *                      CU-count-driven split count (1, or 4+ splits of >= 128 tokens);
  *                      > 0 = split grid with that many splits per sequence (clamped to the
  *                      number of pages of max_seq_len);
  *                      < 0 = balanced schedule with exactly -num_splits workgroups.

@@ -1366,8 +1366,12 @@ int64_t align_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 // interleaved A/B sweeps on MI355X over the five north-star configurations:
 //  * workgroups per CU: one cooperative 4-wave group for D=128 and D=256, two 2-wave groups
 //    for D=64 -- more resident groups contend for HBM without adding bandwidth;
-//  * batches with at least kBalancedMinUnits (sequence, KV head) units take the balanced
-//    single launch (lengths balanced on the device, ~84% of 8 TB/s on Llama-3-8B decode);
+//  * batches with at least kBalancedMinUnits (sequence, KV head) units and a capacity of at
+//    least kBalancedMinCap tokens (or half that with 512+ units) take the balanced single
+//    launch (lengths balanced on the device, ~84% of 8 TB/s on Llama-3-8B decode);
+//  * shorter capacities take the split grid: its one split per unit skips the length scan
+//    and the merges, 15-50% faster below 1 024 tokens (e.g. B=64, Hkv=8, 64 tokens: 7.4 vs
+//    14.9 us);
 //  * fewer, long units (long-context decode) take the split grid, whose page-aligned splits
 //    plus a separate combine beat the balanced merge tree by ~10% there;
 //  * split counts: just enough splits for the workgroup target, each at least
@@ -1376,6 +1380,7 @@ constexpr int64_t kMinTokensPerSplit = 128;   // amortises Q load, pipeline fill
 constexpr int64_t kMaxTokensPerSplit = 16384;  // bounds one workgroup's share of a sequence
 constexpr int64_t kMaxGridDim = 65535;
 constexpr int64_t kBalancedMinUnits = 64;
+constexpr int64_t kBalancedMinCap = 2048;  // tokens of capacity (max_seq_len) for balanced
 constexpr int64_t kFusedMaxSplits = 16;  // split grid: merge in-kernel up to this many splits
 constexpr int64_t kMaxMergeRows = int64_t(1) << 25;  // mx_lse_merge: 64 * rows work-items < 2^31
 
@@ -1484,7 +1489,12 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
     }
     const int64_t units = batch * num_kv_heads * row_tiles;
     ns = ceil_div(num_cus * groups_per_cu(head_dim), units);
-    const int64_t max_by_len = ceil_div(cap, kMinTokensPerSplit);
+    // Every split holds at least kMinTokensPerSplit tokens at capacity, and splitting starts
+    // at four splits: the partial round trip and merge (~3.5 us) are only repaid by cutting a
+    // unit's streaming time at least four ways (capacity 256: 1 split 7.8-8.1 us, 2 splits
+    // 8.7-8.9 us; capacity 512 with 64 units: 4 splits 9.2 us, 1 split 10.2 us).
+    int64_t max_by_len = cap / kMinTokensPerSplit;
+    if (max_by_len < 4) max_by_len = 1;
     if (ns > max_by_len) ns = max_by_len;
     const int64_t min_by_len = ceil_div(cap, kMaxTokensPerSplit);
     if (ns < min_by_len) ns = min_by_len;
@@ -1503,7 +1513,11 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
   plan->chunk_shift = shift;
   const int64_t units = batch * num_kv_heads * row_tiles;
   const bool balanced_ok = batch <= kBalancedMaxBatch && units <= kBalancedMaxUnits;
-  const bool balanced_auto = num_splits == 0 && balanced_ok && units >= kBalancedMinUnits;
+  // Short capacities favour one split per unit (no length scan, no merge): the balanced
+  // schedule pays off from 2 048 tokens, or from 1 024 with at least 512 units.
+  const bool long_enough = cap >= kBalancedMinCap || (cap >= kBalancedMinCap / 2 && units >= 512);
+  const bool balanced_auto =
+      num_splits == 0 && balanced_ok && units >= kBalancedMinUnits && long_enough;
   if ((num_splits < 0 && balanced_ok) || balanced_auto) {
     // Length-balanced single launch (automatic, or num_splits < 0 = that many workgroups).
     int64_t groups;

@@ -194,7 +194,7 @@ def test_split_grid_plan_invariants(B, Hq, Hkv, D, P, max_pages, cap, ns_req):
     (3, 32, 8, 128, -9000, 4095),  # clamped to the 8^4 merge tree
 ])
 def test_balanced_plan(B, Hq, Hkv, D, ns_req, groups):
-    p = plan(B, Hq, Hkv, D, 16, 64, 0, ns_req, num_cus=256)
+    p = plan(B, Hq, Hkv, D, 16, 256, 0, ns_req, num_cus=256)
     assert p["schedule"] == "balanced"
     assert p["workgroups"] == groups and p["splits"] == 0
     slots = groups + B * Hkv
@@ -221,6 +221,23 @@ def test_policy_on_the_north_star_configs():
         sched, n = expect[name]
         assert p["schedule"] == sched, name
         assert (p["workgroups"] if sched == "balanced" else p["splits"]) == n, name
+
+
+@pytest.mark.parametrize("B,Hkv,cap,sched,splits", [
+    (64, 8, 64, "split_grid", 1),       # short capacity: one split per unit, no merge
+    (64, 8, 512, "split_grid", 1),
+    (16, 4, 141, "split_grid", 1),      # 141 tokens: a second split would hold < 128
+    (16, 4, 512, "split_grid", 4),      # 64 units: four 128-token splits fill the CUs
+    (64, 4, 1024, "split_grid", 1),     # 1 024 tokens with 256 units: split grid
+    (64, 8, 1024, "balanced", 0),       # ... with 512 units: balanced
+    (16, 8, 2048, "balanced", 0),       # from 2 048 tokens: balanced
+])
+def test_policy_capacity_gate(B, Hkv, cap, sched, splits):
+    """Batches of short sequences skip the balanced schedule (its length scan and merges cost
+    more than the imbalance they remove below ~2 048 tokens of capacity)."""
+    p = plan(B, 32, Hkv, 128, 16, 512, cap, 0, num_cus=256)
+    assert p["schedule"] == sched
+    assert p["splits"] == splits
 
 
 @pytest.mark.parametrize("SQ,Hq,Hkv,D,groups,group_rows", [
