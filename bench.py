@@ -57,15 +57,23 @@ def _cpu_model() -> str:
 
 
 def _traffic_from_profile(kernel: str, workload: str):
-    """HBM bytes per launch of the main kernel, from the committed rocprofv3 --pmc summary
-    (profiles/<kernel>_<workload>_traffic.md, line 'traffic_bytes_per_launch: N'), or None."""
-    path = os.path.join(PROFILE_DIR, f"{kernel}_{workload}_traffic.md")
-    try:
-        with open(path) as f:
-            m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read())
-        return float(m.group(1)) if m else None
-    except OSError:
-        return None
+    """HBM bytes per launch of the main kernel, from the committed rocprofv3 --pmc summaries:
+    profiles/<kernel>_<workload>_traffic.md (line 'traffic_bytes_per_launch: N') or
+    profiles/traffic_more_configs.md (line 'traffic_bytes_per_launch[<kernel>_<workload>]: N');
+    None when neither covers the workload."""
+    probes = [(f"{kernel}_{workload}_traffic.md", r"traffic_bytes_per_launch:\s*([0-9.eE+]+)"),
+              ("traffic_more_configs.md",
+               r"traffic_bytes_per_launch\[" + re.escape(f"{kernel}_{workload}") +
+               r"\]:\s*([0-9.eE+]+)")]
+    for name, pattern in probes:
+        try:
+            with open(os.path.join(PROFILE_DIR, name)) as f:
+                m = re.search(pattern, f.read())
+        except OSError:
+            continue
+        if m:
+            return float(m.group(1))
+    return None
 
 
 def time_workload(inp: W.DecodeInputs, steps: int, warmup: int, num_splits: int = 0) -> dict:
