@@ -102,15 +102,17 @@ def test_config5_sweep(name):
 # Edge cases of the reference contract
 # ------------------------------------------------------------------------------------------
 
-@pytest.mark.parametrize("P", [16, 64])
+@pytest.mark.parametrize("P", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("D,Hq,Hkv", [(128, 32, 8), (128, 28, 4), (64, 32, 4), (256, 16, 2),
                                        (128, 16, 16), (128, 32, 2)])
 def test_edge_lengths(P, D, Hq, Hkv):
-    # single token, sub-page, page boundary +-1, several pages with tails, full row
+    # single token, sub-page, page boundary +-1, several pages with tails, full row; every
+    # supported page size, on the automatic plan, the split grid (1 and 3 splits) and the
+    # balanced schedule (5 workgroups: units cut into pieces and merged)
     lens = [1, 2, 15, 16, 17, P - 1, P, P + 1, 3 * P + 5, 200, 481, 512]
     spec = W.custom_spec(f"edge_P{P}_D{D}", lens, Hq, Hkv, D, P, pool_pages=0)
     inp = W.make_inputs(spec, seed=1, device=DEV)
-    for ns in (0, 1, 3):
+    for ns in (0, 1, 3, -5):
         out = _decode(inp, num_splits=ns)
         _check(inp, out, label=f"{spec.name} ns={ns}")
 
@@ -397,7 +399,7 @@ def _mq_check(inp, out, causal, label):
 
 @pytest.mark.parametrize("ns", [0, 3, -7])
 @pytest.mark.parametrize("Hq,Hkv,D,P", [(32, 8, 128, 16), (28, 4, 64, 64), (8, 8, 256, 16),
-                                        (32, 2, 128, 32)])
+                                        (32, 2, 128, 32), (16, 2, 64, 256)])
 @pytest.mark.parametrize("sq", [2, 4, 5, 8])
 @pytest.mark.parametrize("causal", [False, True])
 def test_multi_token_queries(causal, sq, Hq, Hkv, D, P, ns):
