@@ -1,7 +1,7 @@
 """Benchmark of the paged GQA decode operator on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload llama3_8b]
-                    [--num-splits 0] [--no-cpu-baseline] [--all] [--shards N]
+                    [--num-splits 0] [--no-cpu-baseline] [--all] [--graph] [--shards N]
 
 One step = one decode-attention call over the whole batch of the workload (default: the
 Llama-3-8B decode shape the metric is quoted on, B=64 Hq=32 Hkv=8 D=128 P=16 L=4096), inputs
@@ -14,6 +14,7 @@ after the second event).  Prints ONE JSON line:
   cpu_baseline  the fp32 oracle (oracle/paged_attention.py) timed on this host on a bounded
              sample of the same workload.
 ``--all`` prints one extra JSON line per north-star configuration (no CPU baseline).
+``--graph`` adds the per-call time of the same calls replayed from a HIP graph.
 ``--shards N`` prints one extra line: the workload's pages cut into N shards, each shard's
 partial decode and the N-way merge timed on this GPU (the per-GPU work of an N-GPU decode).
 """
@@ -76,8 +77,10 @@ def _traffic_from_profile(kernel: str, workload: str):
     return None
 
 
-def time_workload(inp: W.DecodeInputs, steps: int, warmup: int, num_splits: int = 0) -> dict:
-    """Time `steps` calls after `warmup`; events bracket the split-KV kernel of each step."""
+def time_workload(inp: W.DecodeInputs, steps: int, warmup: int, num_splits: int = 0,
+                  graph: bool = False) -> dict:
+    """Time `steps` calls after `warmup`; events bracket the split-KV kernel of each step.
+    With `graph`, also time the same calls captured in a HIP graph and replayed."""
     spec = inp.spec
     stream = torch.cuda.current_stream()
     nbytes = inp.kv_bytes()
@@ -131,6 +134,7 @@ def time_workload(inp: W.DecodeInputs, steps: int, warmup: int, num_splits: int 
         warm = {"us_per_call": round(w_ms * 1e3, 2),
                 "kernel_us_mean": round(statistics.fmean(w_kern), 2),
                 "GBps": round(nbytes / (w_ms * 1e-3) / 1e9, 1)}
+    graphed = time_graph(inp, pools, out, ws, num_splits, steps) if graph else None
     flags = pkg.read_device_status(ws)
     if flags:
         raise RuntimeError(f"device status flags {flags} raised during the benchmark")
@@ -141,6 +145,7 @@ def time_workload(inp: W.DecodeInputs, steps: int, warmup: int, num_splits: int 
         "ms_per_step": ms_per_step,
         "wall_ms_per_step": wall_ms_step,
         "warm": warm,
+        "graph": graphed,
         "kernel_us_mean": kern_mean,
         "kernel_us_median": statistics.median(kern_us),
         "kernel_us_min": min(kern_us),
@@ -148,6 +153,39 @@ def time_workload(inp: W.DecodeInputs, steps: int, warmup: int, num_splits: int 
         "value_gbps": nbytes / (ms_per_step * 1e-3) / 1e9,
         "kernel_gbps": nbytes / (kern_mean * 1e-6) / 1e9,
     }
+
+
+def time_graph(inp: W.DecodeInputs, pools, out, ws, num_splits: int, steps: int) -> dict:
+    """The workload's calls captured in a HIP graph (one call per K/V pool, repeated up to 16
+    calls) and replayed until about `steps` calls ran: the per-call time without host launch
+    overhead.  The library allocates, clears and synchronises nothing inside a call that gets a
+    workspace, and its kernels reset their own counters, so the captured calls replay as is."""
+    spec = inp.spec
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    calls = [pkg.BoundDecode(inp.q, k, v, inp.block_table, inp.seq_lens, inp.scale, out=out,
+                             causal=spec.causal, num_splits=num_splits, workspace=ws,
+                             stream=stream)
+             for k, v in pools]
+    per_graph = len(calls) * max(1, 16 // len(calls))
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(per_graph):
+            calls[i % len(calls)]()
+    torch.cuda.synchronize()
+    replays = max(2, steps // per_graph)
+    cur = torch.cuda.current_stream()
+    g.replay()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(cur)
+    for _ in range(replays):
+        g.replay()
+    end.record(cur)
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / (replays * per_graph)
+    return {"us_per_call": round(us, 2), "GBps": round(inp.kv_bytes() / us / 1e3, 1),
+            "calls_per_graph": per_graph, "replays": replays}
 
 
 def time_append(spec: W.DecodeSpec, steps: int, warmup: int, seed: int = 0) -> dict:
@@ -417,6 +455,9 @@ def result_line(args, spec, r, cpu=None) -> dict:
         },
         "wall_ms_per_step": round(r["wall_ms_per_step"], 5),
     }
+    if r.get("graph") is not None:
+        # The same calls replayed from a HIP graph (no host launch overhead per call).
+        line["graph"] = r["graph"]
     if r["warm"] is not None:
         # Cold (the value above: distinct K/V pools rotate, nothing is served from the 256 MB
         # MALL) against warm (one pool reused).
@@ -442,6 +483,8 @@ def main(argv=None) -> int:
     ap.add_argument("--suite", choices=["c500"], default=None,
                     help="run the reference's 14-case contest suite through run_kernel "
                          "instead of the main workload and print its per-case lines and score")
+    ap.add_argument("--graph", action="store_true",
+                    help="also time the calls captured in a HIP graph and replayed")
     ap.add_argument("--shards", type=int, default=0,
                     help="also time the per-GPU pieces of the workload's decode sharded over N "
                          "GPUs' pages (partial decode per shard + merge), on this one GPU")
@@ -483,7 +526,7 @@ def main(argv=None) -> int:
 
     spec = W.get_spec(args.workload)
     inp = W.make_inputs(spec, seed=args.seed, device="cuda")
-    r = time_workload(inp, args.steps, args.warmup, args.num_splits)
+    r = time_workload(inp, args.steps, args.warmup, args.num_splits, graph=args.graph)
     cpu = None if args.no_cpu_baseline else cpu_baseline(inp, args.cpu_budget)
     line = result_line(args, spec, r, cpu)
     if args.shards > 0:
@@ -506,7 +549,7 @@ def main(argv=None) -> int:
                 continue
             extra = W.make_inputs(name, seed=args.seed, device="cuda")
             steps = max(10, min(args.steps, int(2e11 // max(extra.kv_bytes(), 1))))
-            rr = time_workload(extra, steps, min(args.warmup, steps), 0)
+            rr = time_workload(extra, steps, min(args.warmup, steps), 0, graph=args.graph)
             a2 = argparse.Namespace(**{**vars(args), "steps": steps,
                                        "warmup": min(args.warmup, steps)})
             print(json.dumps(result_line(a2, extra.spec, rr)), flush=True)

@@ -22,9 +22,12 @@
 //    chunk max exceeds it by more than 8); the final O / l uses one max for both, so it is
 //    exact.  Masked chunks (sequence tail, causal limits) use selects, never arithmetic on
 //    unused page slots.
-//  * Two schedules: the split grid (Hkv * row tiles, batch, splits) plus a combine kernel, and
-//    a single length-balanced launch that cuts the batch's chunk line into equal shares on the
-//    device and merges cut units through a fan-in-8 tree of arrival counters.
+//  * Two schedules: the split grid (Hkv * row groups, batch, splits), whose last split per unit
+//    merges the partials in-kernel (up to 16 splits; a combine kernel above that), and a single
+//    length-balanced launch that cuts the batch's chunk line into equal shares on the device
+//    and merges cut units through a fan-in-8 tree of arrival counters.
+//  * Sharded decode: the same kernels can write each query row as fp32 output plus its
+//    log-sum-exp (mx_paged_gqa_decode_partial) for a cross-device merge (mx_lse_merge).
 
 #include <hip/hip_runtime.h>
 
@@ -91,10 +94,6 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
 }
 
-
-// Register image of one 16-token chunk of one KV head.
-//   k[i]    : K[token r16][32*i + 8*g4 .. +7]            (A operand of QK MFMA i)
-//   v[r][w] : V[token 4*g4 + r][(D/16)*r16 + 2w .. +1]   (D/32 dwords per row)
 // Compile-time tuning knobs (defaults are the measured best on MI355X).
 #ifndef MX_NBUF_D64
 #define MX_NBUF_D64 2

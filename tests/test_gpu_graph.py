@@ -1,0 +1,122 @@
+"""The decode under HIP graph capture: captured calls replay to the eager result.
+
+The library issues no allocation, memset or synchronisation inside a call when the caller
+passes a workspace, and the balanced schedule's merge counters and the split grid's arrival
+counters are reset by the kernels themselves, so a captured call (or several back to back in
+one graph) can be replayed.  Each test replays its graph several times with eager work of the
+program in between (other decode calls on the same workspace, in-place updates of q, stream
+synchronisations) and checks every replay against an eager call on the same inputs, bit for bit
+(same plan, same kernels, deterministic merges).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from mx_flash_attn_kernel_opt__amd import (lse_merge, make_workspace, paged_gqa_decode,
+                                           paged_gqa_decode_partial, plan, read_device_status)
+from mx_flash_attn_kernel_opt__amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _inputs(lens, Hq, Hkv, D, P, sq=1, seed=0):
+    return W.make_inputs(W.custom_spec("graph", lens, Hq, Hkv, D, P, seqlen_q=sq), seed=seed,
+                         device=DEV)
+
+
+def _workspace(inp, num_splits):
+    s = inp.spec
+    p = plan(s.batch, s.num_heads, s.num_kv_heads, s.head_dim, s.page_size, s.max_pages, 0,
+             num_splits, seqlen_q=s.seqlen_q)
+    return make_workspace(p["workspace_bytes"], DEV), p
+
+
+@pytest.mark.parametrize("num_splits,schedule,launches", [
+    (0, "balanced", 1),      # merge tree with arrival counters reset in-kernel
+    (4, "split_grid", 1),    # last split merges (arrival counter reset by it)
+    (32, "split_grid", 2),   # split kernel + combine kernel
+    (1, "split_grid", 1),
+])
+@pytest.mark.parametrize("sq,causal", [(1, False), (4, True)])
+def test_captured_decode_replays_to_the_eager_result(num_splits, schedule, launches, sq, causal):
+    lens = [1, 17, 300, 2500, 4096, 0, 999] + [1500] * 9
+    inp = _inputs(lens, 32, 8, 128, 16, sq=sq, seed=num_splits + sq)
+    ws, p = _workspace(inp, num_splits)
+    assert p["schedule"] == schedule and p["launches"] == launches
+    out = torch.empty_like(inp.q)
+    kw = dict(out=out, causal=causal, num_splits=num_splits, workspace=ws)
+
+    def eager():
+        r = paged_gqa_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_table, inp.seq_lens,
+                             inp.scale, **{**kw, "out": torch.empty_like(inp.q)})
+        torch.cuda.synchronize()
+        return r.clone()
+
+    expect = eager()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):          # warm-up on the capture stream
+        paged_gqa_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_table, inp.seq_lens,
+                         inp.scale, **kw)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(3):                   # three calls per replay: counters must reset
+            paged_gqa_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_table, inp.seq_lens,
+                             inp.scale, **kw)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, expect), f"replay {rep}"
+        # eager work of the program between replays, on the same workspace
+        other = eager()
+        assert torch.equal(other, expect)
+        if rep == 1:
+            # the graph reads q at replay time: update it in place and re-derive the expectation
+            inp.q.mul_(-1.0)
+            expect = eager()
+    assert read_device_status(ws) == 0
+
+
+def test_captured_partial_decode_and_merge_replay():
+    """Sharded decode captured as one graph: two shards' partial decodes and their merge."""
+    from mx_flash_attn_kernel_opt__amd import shard_pages
+    inp = _inputs([5000, 33, 2048, 700] * 4, 32, 8, 128, 16, seed=9)
+    shards = shard_pages(inp.block_table, inp.seq_lens, 16, 2)
+    ws, _ = _workspace(inp, 0)
+    o = torch.empty((2,) + tuple(inp.q.shape), dtype=torch.float32, device=DEV)
+    lse = torch.empty(o.shape[:-1], dtype=torch.float32, device=DEV)
+    out = torch.empty_like(inp.q)
+
+    def run():
+        for s, (t, l) in enumerate(shards):
+            po, pl = paged_gqa_decode_partial(inp.q, inp.k_cache, inp.v_cache, t, l, inp.scale,
+                                              workspace=ws)
+            o[s].copy_(po)
+            lse[s].copy_(pl)
+        lse_merge(o, lse, out=out)
+
+    run()
+    torch.cuda.synchronize()
+    expect = out.clone()
+    # the partial entry point allocates its outputs with torch; capture them in the graph's pool
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, expect), f"replay {rep}"
+        full = paged_gqa_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_table, inp.seq_lens,
+                                inp.scale, workspace=ws)
+        torch.cuda.synchronize()
+        assert (full.float() - expect.float()).abs().max().item() <= 2e-2
