@@ -1393,6 +1393,8 @@ int64_t groups_per_cu(int64_t head_dim) { return head_dim == 64 ? 2 : 1; }
 constexpr int64_t kBalancedMaxBatch = 512;
 constexpr int64_t kBalancedMaxGroups = 4095;  // pieces per unit stay within the 8^4 merge tree
 constexpr int64_t kBalancedMaxUnits = 8192;   // batch * Hkv * row tiles (counter region)
+// The balanced kernels count a batch's chunks (plus per-unit overheads) in 32-bit integers.
+constexpr int64_t kBalancedMaxLine = int64_t(1) << 30;
 
 struct Plan {
   int schedule = MX_SCHEDULE_SPLIT_GRID;
@@ -1511,7 +1513,8 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
   while ((int64_t(kChunk) << shift) < page_size) ++shift;
   plan->chunk_shift = shift;
   const int64_t units = batch * num_kv_heads * row_tiles;
-  const bool balanced_ok = batch <= kBalancedMaxBatch && units <= kBalancedMaxUnits;
+  const bool balanced_ok = batch <= kBalancedMaxBatch && units <= kBalancedMaxUnits &&
+                           units * (ceil_div(cap, kChunk) + MX_UNIT_OVERHEAD) < kBalancedMaxLine;
   // Short capacities favour one split per unit (no length scan, no merge): the balanced
   // schedule pays off from 2 048 tokens, or from 1 024 with at least 512 units.
   const bool long_enough = cap >= kBalancedMinCap || (cap >= kBalancedMinCap / 2 && units >= 512);
@@ -1544,8 +1547,8 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
   }
   if (num_splits < 0)
     return fail(MX_STATUS_UNSUPPORTED,
-                "the balanced schedule supports batch <= 512 and batch * num_kv_heads * "
-                "ceil(seqlen_q * group / 16) <= 8192");
+                "the balanced schedule supports batch <= 512, batch * num_kv_heads * row "
+                "groups <= 8192 and fewer than 2^30 chunks of capacity over all units");
   if (ns > 1) {
     const int64_t prow = batch * seqlen_q * num_heads * ns;
     plan->lse_offset = kPartialBase;

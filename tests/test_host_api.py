@@ -384,3 +384,16 @@ def test_shard_pages_rejects_bad_arguments():
         shard_pages(table, lens, 16, 2, seqlen_q=0)
     with pytest.raises(ValueError):
         shard_pages(table, lens[:1], 16, 2)
+
+
+def test_balanced_schedule_bounds_its_32_bit_chunk_line():
+    """The balanced kernel counts the batch's chunks in 32-bit integers: plans whose units times
+    capacity chunks reach 2^30 take the split grid, and forcing the balanced schedule fails."""
+    # 512 x 16 units of 4M tokens (262 144 chunks each): 2^31 chunks of capacity
+    p = plan(512, 16, 16, 128, 256, 16384, 0, 0, num_cus=256)
+    assert p["schedule"] == "split_grid"
+    with pytest.raises(MXAttnError) as e:
+        plan(512, 16, 16, 128, 256, 16384, 0, -10, num_cus=256)
+    assert e.value.status == _lib.MX_STATUS_UNSUPPORTED
+    # the same batch with a 64K-token capacity stays balanced
+    assert plan(512, 16, 16, 128, 256, 16384, 65536, 0, num_cus=256)["schedule"] == "balanced"
