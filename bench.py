@@ -43,6 +43,7 @@ from mx_flash_attn_kernel_opt__amd import workloads as W  # noqa: E402
 METRIC = "decode attn µs/call + effective KV HBM GB/s (% of MI355X peak), 1 GPU"
 HBM_PEAK_GBPS = 8000.0
 MALL_BYTES = 256 * 1024 * 1024
+MAX_POOL_COPIES = 256   # tiny configurations: up to 256 pool copies (config 1: 154 x 17 MB)
 PROFILE_DIR = os.path.join(REPO, "profiles")
 
 
@@ -84,8 +85,10 @@ def time_workload(inp: W.DecodeInputs, steps: int, warmup: int, num_splits: int 
     spec = inp.spec
     stream = torch.cuda.current_stream()
     nbytes = inp.kv_bytes()
-    # Rotate distinct copies of the KV pool when one would fit in the 256 MB MALL.
-    copies = 1 if nbytes >= 3 * MALL_BYTES else min(8, max(2, math.ceil(3 * MALL_BYTES / nbytes)))
+    # Rotate distinct copies of the KV pool when one would fit in the 256 MB MALL: enough that
+    # the K/V bytes of the rotation exceed three MALLs, so a call never finds its pages there.
+    copies = (1 if nbytes >= 3 * MALL_BYTES
+              else min(MAX_POOL_COPIES, max(2, math.ceil(3 * MALL_BYTES / max(nbytes, 1)))))
     pools = [(inp.k_cache, inp.v_cache)] + [(inp.k_cache.clone(), inp.v_cache.clone())
                                             for _ in range(copies - 1)]
     plan = pkg.plan(spec.batch, spec.num_heads, spec.num_kv_heads, spec.head_dim,
