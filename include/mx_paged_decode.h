@@ -115,6 +115,8 @@ void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_pa
  *                      zero); NULL = library-owned.
  *   phase              0, MX_PHASE_MAIN_ONLY or MX_PHASE_COMBINE_ONLY.
  *   stream             hipStream_t (NULL = legacy default stream).
+ * q, k_cache and v_cache must be 16-byte aligned and out 8-byte aligned (MX_STATUS_INVALID_ARGUMENT
+ * otherwise).
  * Returns MX_STATUS_OK or a negative MX_STATUS_* code; nothing is launched on error.
  */
 int mx_paged_gqa_decode(const void* q, const void* k_cache, const void* v_cache, void* out,

@@ -1742,6 +1742,12 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* o
                 void* workspace, int64_t workspace_bytes, int32_t phase, void* stream) {
   if (phase != 0 && phase != MX_PHASE_MAIN_ONLY && phase != MX_PHASE_COMBINE_ONLY)
     return fail(MX_STATUS_INVALID_ARGUMENT, "phase must be 0, 1 or 2");
+  // The kernels read q, K and V rows as 16-byte vectors and write out in 8-byte pieces.
+  for (const void* p : {q, k_cache, v_cache})
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
+      return fail(MX_STATUS_INVALID_ARGUMENT, "q, k_cache and v_cache must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(out) % 8 != 0)
+    return fail(MX_STATUS_INVALID_ARGUMENT, "out must be 8-byte aligned");
   if (causal != 0 && causal != 1) return fail(MX_STATUS_INVALID_ARGUMENT, "causal must be 0 or 1");
   if (!std::isfinite(scale)) return fail(MX_STATUS_INVALID_ARGUMENT, "scale must be finite");
   if (num_pages < 0) return fail(MX_STATUS_INVALID_SHAPE, "num_pages must be >= 0");

@@ -108,6 +108,10 @@ def test_null_pointers_are_rejected(field):
     (dict(scale=float("nan")), _lib.MX_STATUS_INVALID_ARGUMENT),
     (dict(scale=float("inf")), _lib.MX_STATUS_INVALID_ARGUMENT),
     (dict(ws_bytes=100), _lib.MX_STATUS_WORKSPACE_TOO_SMALL),
+    (dict(q=ctypes.c_void_p(0x1008)), _lib.MX_STATUS_INVALID_ARGUMENT),   # 16-byte loads
+    (dict(k=ctypes.c_void_p(0x1004)), _lib.MX_STATUS_INVALID_ARGUMENT),
+    (dict(v=ctypes.c_void_p(0x1002)), _lib.MX_STATUS_INVALID_ARGUMENT),
+    (dict(out=ctypes.c_void_p(0x1004)), _lib.MX_STATUS_INVALID_ARGUMENT),  # 8-byte stores
 ])
 def test_invalid_arguments_return_status(over, status):
     assert _decode(**over) == status
