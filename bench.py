@@ -28,6 +28,7 @@ import math
 import os
 import re
 import statistics
+import subprocess
 import sys
 import time
 
@@ -547,17 +548,23 @@ def main(argv=None) -> int:
         del src, dst
         torch.cuda.empty_cache()
     if args.all:
+        # Every other configuration in a fresh child process: measured late in one process,
+        # after multi-GB allocations and frees, the same kernel ran up to 8 % slower.
         for name in list(W.NORTH_STAR) + list(W.EXTRA):
             if name == spec.name:
                 continue
-            extra = W.make_inputs(name, seed=args.seed, device="cuda")
-            steps = max(10, min(args.steps, int(2e11 // max(extra.kv_bytes(), 1))))
-            rr = time_workload(extra, steps, min(args.warmup, steps), 0, graph=args.graph)
-            a2 = argparse.Namespace(**{**vars(args), "steps": steps,
-                                       "warmup": min(args.warmup, steps)})
-            print(json.dumps(result_line(a2, extra.spec, rr)), flush=True)
-            del extra
-            torch.cuda.empty_cache()
+            es = W.get_spec(name)
+            lens = W._make_seq_lens(es, torch.Generator().manual_seed(args.seed))
+            nbytes = W.kv_bytes(lens, es.num_kv_heads, es.head_dim)
+            steps = max(10, min(args.steps, int(2e11 // max(nbytes, 1))))
+            cmd = [sys.executable, os.path.abspath(__file__), "--workload", name, "--steps",
+                   str(steps), "--warmup", str(min(args.warmup, steps)), "--seed",
+                   str(args.seed), "--no-cpu-baseline"] + (["--graph"] if args.graph else [])
+            child = subprocess.run(cmd, capture_output=True, text=True)
+            lines = [ln for ln in child.stdout.splitlines() if ln.startswith("{")]
+            if child.returncode != 0 or not lines:
+                raise RuntimeError(f"bench of {name} failed:\n{child.stderr[-2000:]}")
+            print(lines[-1], flush=True)
         print(json.dumps(time_append(W.get_spec(W.BENCH_DEFAULT), 200, 20, args.seed)),
               flush=True)
     print(json.dumps(line), flush=True)
