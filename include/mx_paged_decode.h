@@ -212,6 +212,29 @@ int mx_paged_kv_append(const void* k_new, const void* v_new, void* k_cache, void
                        int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
                        void* workspace, void* stream);
 
+/*
+ * Append-and-attend: the step flash_attn_with_kvcache performs when given k / v (the
+ * reference's oracle, called with k = v = None by its harness, verify_real.py:40-41).  Writes
+ * k_new / v_new [batch, seqlen_new, num_kv_heads, head_dim] bf16 at positions
+ * max(seq_lens[b], 0) + j of each sequence's block-table row (as mx_paged_kv_append), then
+ * decodes q over the max(seq_lens[b], 0) + seqlen_new keys of each sequence (with causal = 1,
+ * query token i of seqlen_q sees keys t < L_new - seqlen_q + i + 1, L_new the count after the
+ * append).  seq_lens are the lengths BEFORE the append and are not modified.  Other arguments
+ * as mx_paged_gqa_decode (max_seq_len is the capacity after the append) and
+ * mx_paged_kv_append (num_pages is required; slots past the table row or outside the pool are
+ * skipped and flagged, and those keys are not attended).  The workspace is the decode's
+ * (mx_paged_gqa_decode_workspace_size).  Nothing is launched on error.  Returns MX_STATUS_*.
+ * No counterpart in the reference's own code; the semantics are flash_attn_with_kvcache's.
+ */
+int mx_paged_gqa_decode_append(const void* q, const void* k_new, const void* v_new,
+                               void* k_cache, void* v_cache, void* out, const int32_t* seq_lens,
+                               const int32_t* block_table, int64_t batch, int64_t seqlen_q,
+                               int64_t seqlen_new, int64_t num_heads, int64_t num_kv_heads,
+                               int64_t head_dim, int64_t page_size, int64_t num_pages,
+                               int64_t max_pages_per_seq, int64_t max_seq_len, int32_t causal,
+                               float scale, int64_t num_splits, void* workspace,
+                               int64_t workspace_bytes, void* stream);
+
 /* Copies the sticky device status word (MX_DEVICE_* bits) of a workspace (NULL = the library's
  * workspace of the current device) to *flags_out after synchronising the stream; clears it
  * when reset != 0.  Not part of the reference (which validates nothing on the device). */

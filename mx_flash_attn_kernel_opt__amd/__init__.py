@@ -12,6 +12,7 @@ from .decode import (  # noqa: F401
     lse_merge,
     make_workspace,
     paged_gqa_decode,
+    paged_gqa_decode_append,
     paged_gqa_decode_partial,
     paged_kv_append,
     plan,
@@ -29,6 +30,7 @@ __all__ = [
     "lse_merge",
     "make_workspace",
     "paged_gqa_decode",
+    "paged_gqa_decode_append",
     "paged_gqa_decode_partial",
     "paged_kv_append",
     "plan",

@@ -403,12 +403,22 @@ struct MainShape {
   // normalised output to o_out and its natural-log sum-exp to lse_out instead of bf16 to out.
   float* o_out;
   float* lse_out;
+  // Append-and-attend: seq_lens are lengths before an append of this many tokens per sequence
+  // (written by the append kernel just before), so sequence b has max(seq_lens[b], 0) + appended
+  // keys.  0 = seq_lens are the key counts.
+  int appended;
 };
+
+// Keys of sequence b before clamping (see MainShape::appended).
+__device__ __forceinline__ int key_count(const int32_t* seq_lens, int b, int appended) {
+  const int L = seq_lens[b];
+  return appended > 0 ? max(L, 0) + appended : L;
+}
 
 // Sequence length as the kernels see it: clamped to the planned capacity (flagged).
 __device__ __forceinline__ int clamped_len(const int32_t* seq_lens, int b, const MainShape& sh,
                                            uint32_t* status, bool report) {
-  int seq = seq_lens[b];
+  int seq = key_count(seq_lens, b, sh.appended);
   if (seq > sh.cap_tokens) {
     if (report) atomicOr(status, (uint32_t)MX_DEVICE_SEQ_TOO_LONG);
     seq = sh.cap_tokens;
@@ -942,7 +952,7 @@ void mx_paged_decode_balanced(
   // Empty sequences (L <= 0) are defined as zero output; sequence b's zeros (its seqlen_q *
   // num_heads consecutive rows) are written by workgroup b % num_groups.
   for (int b = wg; b < B; b += sh.num_groups) {
-    if (seq_lens[b] <= 0) {
+    if (key_count(seq_lens, b, sh.appended) <= 0) {
       const int64_t row0 = (int64_t)b * sh.seqlen_q * sh.num_heads;
       for (int e = tid; e < sh.seqlen_q * sh.num_heads * (D / 4); e += 64 * NW)
         store_row4<D>(out, sh, row0 + e / (D / 4), 4 * (e % (D / 4)), f32x4{0.f, 0.f, 0.f, 0.f},
@@ -1271,12 +1281,12 @@ __global__ __launch_bounds__(64) void mx_paged_decode_combine(
     const float* __restrict__ part_o, const float* __restrict__ part_lse,
     const int32_t* __restrict__ seq_lens, uint16_t* __restrict__ out, float* __restrict__ o_out,
     float* __restrict__ lse_out, int num_heads, int seqlen_q, int num_splits,
-    int tokens_per_split, int cap_tokens) {
+    int tokens_per_split, int cap_tokens, int appended) {
   const int h = blockIdx.x;
   const int bt = blockIdx.y;  // sequence * seqlen_q + query token
   const int b = bt / seqlen_q;
   const int lane = threadIdx.x;
-  const int seq = min(seq_lens[b], cap_tokens);
+  const int seq = min(key_count(seq_lens, b, appended), cap_tokens);
   if (seq <= tokens_per_split) return;  // single split (or empty): main kernel wrote it
   const int nsv = (seq + tokens_per_split - 1) / tokens_per_split;
   const int64_t row = (int64_t)bt * num_heads + h;
@@ -1609,7 +1619,7 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
                   const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
                   int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads, int64_t page_size,
                   int64_t num_pages, int64_t max_pages, float scale, char* ws, int32_t phase,
-                  float* o_out, float* lse_out, hipStream_t stream) {
+                  float* o_out, float* lse_out, int appended, hipStream_t stream) {
   constexpr int kNW = waves_per_group<D>();
   constexpr int kNBUF = ring_depth<D>();
   MainShape sh;
@@ -1638,6 +1648,7 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   sh.num_slots = (int)plan.slots;
   sh.o_out = o_out;
   sh.lse_out = lse_out;
+  sh.appended = appended;
   uint32_t* status = reinterpret_cast<uint32_t*>(ws);
 
   if (plan.schedule == MX_SCHEDULE_BALANCED) {
@@ -1680,7 +1691,7 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
     hipLaunchKernelGGL(mx_paged_decode_combine<D>, grid, dim3(64), 0, stream, part_o, part_lse,
                        seq_lens, static_cast<uint16_t*>(out), o_out, lse_out, (int)num_heads,
                        (int)seqlen_q, (int)plan.splits, (int)plan.tokens_per_split,
-                       (int)plan.cap_tokens);
+                       (int)plan.cap_tokens, appended);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -1732,14 +1743,13 @@ int64_t mx_paged_gqa_decode_workspace_size(int64_t batch, int64_t seqlen_q, int6
 
 namespace {
 
-// Shared by mx_paged_gqa_decode (bf16 into out) and mx_paged_gqa_decode_partial (fp32 rows into
-// o_out and natural-log sum-exps into lse_out; out is then null).
-int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* out, float* o_out,
-                float* lse_out, const int32_t* seq_lens, const int32_t* block_table,
-                int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads,
-                int64_t head_dim, int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
-                int64_t max_seq_len, int32_t causal, float scale, int64_t num_splits,
-                void* workspace, int64_t workspace_bytes, int32_t phase, void* stream) {
+// Argument checks, plan and workspace of a decode call; launches nothing.
+int prepare_decode(const void* q, const void* k_cache, const void* v_cache, const void* out,
+                   int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads,
+                   int64_t head_dim, int64_t page_size, int64_t num_pages,
+                   int64_t max_pages_per_seq, int64_t max_seq_len, int32_t causal, float scale,
+                   int64_t num_splits, void** workspace, int64_t workspace_bytes,
+                   int32_t phase, Plan* plan) {
   if (phase != 0 && phase != MX_PHASE_MAIN_ONLY && phase != MX_PHASE_COMBINE_ONLY)
     return fail(MX_STATUS_INVALID_ARGUMENT, "phase must be 0, 1 or 2");
   // The kernels read q, K and V rows as 16-byte vectors and write out in 8-byte pieces.
@@ -1751,19 +1761,27 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* o
   if (causal != 0 && causal != 1) return fail(MX_STATUS_INVALID_ARGUMENT, "causal must be 0 or 1");
   if (!std::isfinite(scale)) return fail(MX_STATUS_INVALID_ARGUMENT, "scale must be finite");
   if (num_pages < 0) return fail(MX_STATUS_INVALID_SHAPE, "num_pages must be >= 0");
-  Plan plan;
   int st = make_plan(batch, seqlen_q, num_heads, num_kv_heads, head_dim, page_size,
-                     max_pages_per_seq, max_seq_len, num_splits, 0, &plan);
+                     max_pages_per_seq, max_seq_len, num_splits, 0, plan);
   if (st != MX_STATUS_OK) return st;
-  if (workspace != nullptr) {
-    if (workspace_bytes < plan.workspace_bytes)
+  if (*workspace != nullptr) {
+    if (workspace_bytes < plan->workspace_bytes)
       return fail(MX_STATUS_WORKSPACE_TOO_SMALL,
                   "workspace_bytes " + std::to_string(workspace_bytes) + " < required " +
-                      std::to_string(plan.workspace_bytes));
-  } else {
-    st = internal_workspace(plan.workspace_bytes, &workspace);
-    if (st != MX_STATUS_OK) return st;
+                      std::to_string(plan->workspace_bytes));
+    return MX_STATUS_OK;
   }
+  return internal_workspace(plan->workspace_bytes, workspace);
+}
+
+// Launches a prepared decode: bf16 into out, or (partial outputs) fp32 rows into o_out and
+// natural-log sum-exps into lse_out (out is then null).  `appended`: see MainShape.
+int run_decode(const Plan& plan, const void* q, const void* k_cache, const void* v_cache,
+               void* out, float* o_out, float* lse_out, const int32_t* seq_lens,
+               const int32_t* block_table, int64_t batch, int64_t seqlen_q, int64_t num_heads,
+               int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_pages,
+               int64_t max_pages_per_seq, int32_t causal, float scale, void* workspace,
+               int32_t phase, int32_t appended, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   hipError_t e;
@@ -1772,7 +1790,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* o
 #define MX_LAUNCH(DIM, CAUSAL, KT)                                                            \
   launch<DIM, CAUSAL, KT>(plan, q, k_cache, v_cache, out, seq_lens, block_table, batch, seqlen_q, \
                       num_heads, num_kv_heads, page_size, num_pages, max_pages_per_seq, scale, \
-                      ws, phase, o_out, lse_out, s)
+                      ws, phase, o_out, lse_out, appended, s)
   const bool pair = plan.tiles_per_group == 2;
   switch (head_dim) {
     case 64:
@@ -1788,6 +1806,73 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* o
       break;
   }
 #undef MX_LAUNCH
+  if (e != hipSuccess)
+    return fail(MX_STATUS_HIP_ERROR, std::string("kernel launch failed: ") + hipGetErrorString(e));
+  return ok();
+}
+
+// Shared by mx_paged_gqa_decode (bf16 into out) and mx_paged_gqa_decode_partial (fp32 rows into
+// o_out and natural-log sum-exps into lse_out; out is then null).
+int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* out, float* o_out,
+                float* lse_out, const int32_t* seq_lens, const int32_t* block_table,
+                int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads,
+                int64_t head_dim, int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
+                int64_t max_seq_len, int32_t causal, float scale, int64_t num_splits,
+                void* workspace, int64_t workspace_bytes, int32_t phase, void* stream) {
+  Plan plan;
+  const int st = prepare_decode(q, k_cache, v_cache, out, batch, seqlen_q, num_heads,
+                                num_kv_heads, head_dim, page_size, num_pages, max_pages_per_seq,
+                                max_seq_len, causal, scale, num_splits, &workspace,
+                                workspace_bytes, phase, &plan);
+  if (st != MX_STATUS_OK) return st;
+  return run_decode(plan, q, k_cache, v_cache, out, o_out, lse_out, seq_lens, block_table, batch,
+                    seqlen_q, num_heads, num_kv_heads, head_dim, page_size, num_pages,
+                    max_pages_per_seq, causal, scale, workspace, phase, 0, stream);
+}
+
+// Argument checks of a paged K/V append (shared by mx_paged_kv_append and the fused
+// append-and-attend entry); launches nothing.
+int check_append(const void* k_new, const void* v_new, const void* k_cache, const void* v_cache,
+                 const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
+                 int64_t seqlen_new, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                 int64_t num_pages, int64_t max_pages_per_seq) {
+  // k_new / v_new may be NULL (an empty tensor) only when there is nothing to append.
+  if ((seqlen_new > 0 && (!k_new || !v_new)) || !k_cache || !v_cache || !seq_lens ||
+      !block_table)
+    return fail(MX_STATUS_NULL_POINTER,
+                "k_new, v_new, k_cache, v_cache, seq_lens and block_table must be non-NULL");
+  for (const void* p : {k_new, v_new, k_cache, v_cache})
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
+      return fail(MX_STATUS_INVALID_ARGUMENT, "K/V tensors must be 16-byte aligned");
+  if (batch < 1 || seqlen_new < 0 || num_kv_heads < 1 || head_dim < 1 || page_size < 1 ||
+      max_pages_per_seq < 1)
+    return fail(MX_STATUS_INVALID_SHAPE,
+                "batch, num_kv_heads, head_dim, page_size and max_pages_per_seq must be >= 1 "
+                "and seqlen_new >= 0");
+  if (num_pages < 1)
+    return fail(MX_STATUS_INVALID_SHAPE,
+                "num_pages (the pool size) must be >= 1: it bounds every write");
+  if (head_dim % 8 != 0) return fail(MX_STATUS_UNSUPPORTED, "head_dim must be a multiple of 8");
+  if (max_pages_per_seq > (int64_t)INT32_MAX / page_size || num_pages > INT32_MAX ||
+      num_kv_heads * head_dim > INT32_MAX / 8 ||
+      batch * seqlen_new > (int64_t)INT32_MAX / 2 - 4)
+    return fail(MX_STATUS_UNSUPPORTED, "sizes must fit 32-bit indices");
+  return MX_STATUS_OK;
+}
+
+int launch_append(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                  const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
+                  int64_t seqlen_new, int64_t num_kv_heads, int64_t head_dim,
+                  int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
+                  void* workspace, void* stream) {
+  const int64_t waves = 2 * batch * seqlen_new;
+  hipLaunchKernelGGL(mx_paged_kv_append_kernel, dim3((unsigned)ceil_div(waves, 4)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(k_new),
+                     static_cast<const uint16_t*>(v_new), static_cast<uint16_t*>(k_cache),
+                     static_cast<uint16_t*>(v_cache), seq_lens, block_table, (int)batch,
+                     (int)seqlen_new, (int)(num_kv_heads * head_dim / 8), (int)page_size,
+                     (int)num_pages, (int)max_pages_per_seq, static_cast<uint32_t*>(workspace));
+  const hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return fail(MX_STATUS_HIP_ERROR, std::string("kernel launch failed: ") + hipGetErrorString(e));
   return ok();
@@ -1932,42 +2017,48 @@ int mx_paged_kv_append(const void* k_new, const void* v_new, void* k_cache, void
                        int64_t seqlen_new, int64_t num_kv_heads, int64_t head_dim,
                        int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
                        void* workspace, void* stream) {
-  if (!k_new || !v_new || !k_cache || !v_cache || !seq_lens || !block_table)
-    return fail(MX_STATUS_NULL_POINTER,
-                "k_new, v_new, k_cache, v_cache, seq_lens and block_table must be non-NULL");
-  for (const void* p : {k_new, v_new, static_cast<const void*>(k_cache),
-                        static_cast<const void*>(v_cache)})
-    if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
-      return fail(MX_STATUS_INVALID_ARGUMENT, "K/V tensors must be 16-byte aligned");
-  if (batch < 1 || seqlen_new < 0 || num_kv_heads < 1 || head_dim < 1 || page_size < 1 ||
-      max_pages_per_seq < 1)
-    return fail(MX_STATUS_INVALID_SHAPE,
-                "batch, num_kv_heads, head_dim, page_size and max_pages_per_seq must be >= 1 "
-                "and seqlen_new >= 0");
-  if (num_pages < 1)
-    return fail(MX_STATUS_INVALID_SHAPE,
-                "num_pages (the pool size) must be >= 1: it bounds every write");
-  if (head_dim % 8 != 0) return fail(MX_STATUS_UNSUPPORTED, "head_dim must be a multiple of 8");
-  if (max_pages_per_seq > (int64_t)INT32_MAX / page_size || num_pages > INT32_MAX ||
-      num_kv_heads * head_dim > INT32_MAX / 8 ||
-      batch * seqlen_new > (int64_t)INT32_MAX / 2 - 4)
-    return fail(MX_STATUS_UNSUPPORTED, "sizes must fit 32-bit indices");
+  int st = check_append(k_new, v_new, k_cache, v_cache, seq_lens, block_table, batch, seqlen_new,
+                        num_kv_heads, head_dim, page_size, num_pages, max_pages_per_seq);
+  if (st != MX_STATUS_OK) return st;
   if (seqlen_new == 0) return ok();
   if (workspace == nullptr) {
-    const int st = internal_workspace(kStatusBytes, &workspace);
+    st = internal_workspace(kStatusBytes, &workspace);
     if (st != MX_STATUS_OK) return st;
   }
-  const int64_t waves = 2 * batch * seqlen_new;
-  hipLaunchKernelGGL(mx_paged_kv_append_kernel, dim3((unsigned)ceil_div(waves, 4)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(k_new),
-                     static_cast<const uint16_t*>(v_new), static_cast<uint16_t*>(k_cache),
-                     static_cast<uint16_t*>(v_cache), seq_lens, block_table, (int)batch,
-                     (int)seqlen_new, (int)(num_kv_heads * head_dim / 8), (int)page_size,
-                     (int)num_pages, (int)max_pages_per_seq, static_cast<uint32_t*>(workspace));
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess)
-    return fail(MX_STATUS_HIP_ERROR, std::string("kernel launch failed: ") + hipGetErrorString(e));
-  return ok();
+  return launch_append(k_new, v_new, k_cache, v_cache, seq_lens, block_table, batch, seqlen_new,
+                       num_kv_heads, head_dim, page_size, num_pages, max_pages_per_seq,
+                       workspace, stream);
+}
+
+int mx_paged_gqa_decode_append(const void* q, const void* k_new, const void* v_new,
+                               void* k_cache, void* v_cache, void* out, const int32_t* seq_lens,
+                               const int32_t* block_table, int64_t batch, int64_t seqlen_q,
+                               int64_t seqlen_new, int64_t num_heads, int64_t num_kv_heads,
+                               int64_t head_dim, int64_t page_size, int64_t num_pages,
+                               int64_t max_pages_per_seq, int64_t max_seq_len, int32_t causal,
+                               float scale, int64_t num_splits, void* workspace,
+                               int64_t workspace_bytes, void* stream) {
+  if (!q || !out)
+    return fail(MX_STATUS_NULL_POINTER, "q and out must be non-NULL");
+  int st = check_append(k_new, v_new, k_cache, v_cache, seq_lens, block_table, batch, seqlen_new,
+                        num_kv_heads, head_dim, page_size, num_pages, max_pages_per_seq);
+  if (st != MX_STATUS_OK) return st;
+  if (seqlen_new > INT32_MAX / 2)
+    return fail(MX_STATUS_UNSUPPORTED, "seqlen_new must be < 2^30");
+  Plan plan;
+  st = prepare_decode(q, k_cache, v_cache, out, batch, seqlen_q, num_heads, num_kv_heads,
+                      head_dim, page_size, num_pages, max_pages_per_seq, max_seq_len, causal,
+                      scale, num_splits, &workspace, workspace_bytes, 0, &plan);
+  if (st != MX_STATUS_OK) return st;
+  if (seqlen_new > 0) {
+    st = launch_append(k_new, v_new, k_cache, v_cache, seq_lens, block_table, batch, seqlen_new,
+                       num_kv_heads, head_dim, page_size, num_pages, max_pages_per_seq,
+                       workspace, stream);
+    if (st != MX_STATUS_OK) return st;
+  }
+  return run_decode(plan, q, k_cache, v_cache, out, nullptr, nullptr, seq_lens, block_table,
+                    batch, seqlen_q, num_heads, num_kv_heads, head_dim, page_size, num_pages,
+                    max_pages_per_seq, causal, scale, workspace, 0, (int32_t)seqlen_new, stream);
 }
 
 int mx_last_status(void) { return g_last_status; }

@@ -323,6 +323,52 @@ def paged_kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Ten
     _lib.check(st)
 
 
+def paged_gqa_decode_append(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                            k_cache: torch.Tensor, v_cache: torch.Tensor,
+                            block_table: torch.Tensor, seq_lens: torch.Tensor,
+                            scale: float | None = None, *, out: torch.Tensor | None = None,
+                            causal: bool = False, num_splits: int = 0, max_seq_len: int = 0,
+                            workspace: torch.Tensor | None = None,
+                            stream=None) -> torch.Tensor:
+    """Append the new tokens' K/V to the paged cache, then decode over the cache including them
+    (flash_attn_with_kvcache with k / v given).
+
+    k_new / v_new: [B, S, Hkv, D] (or [B, Hkv, D] for S = 1) bf16, written at positions
+    max(seq_lens[b], 0) + j; seq_lens are the lengths before the append and are not modified
+    (add S before the next call).  q: [B, Hq, D] or [B, seqlen_q, Hq, D]; with ``causal`` query
+    token i sees keys t < L + S - seqlen_q + i + 1.  Returns the bf16 output shaped like q.
+    """
+    dev, B, SQ, Hq, D, num_pages, P, Hkv = _check_decode_inputs(q, k_cache, v_cache,
+                                                                block_table, seq_lens)
+    _require(k_new.shape == v_new.shape, "k_new and v_new must have the same shape")
+    for name, t in (("k_new", k_new), ("v_new", v_new)):
+        _require(t.device == dev and t.dtype == torch.bfloat16 and t.is_contiguous(),
+                 f"{name} must be a contiguous bf16 tensor on {dev}")
+    if k_new.dim() == 3:
+        S = 1
+        _require(tuple(k_new.shape) == (B, Hkv, D), "k_new must be [B, Hkv, D] or [B, S, Hkv, D]")
+    else:
+        _require(k_new.dim() == 4 and k_new.shape[0] == B and tuple(k_new.shape[2:]) == (Hkv, D),
+                 "k_new must be [B, Hkv, D] or [B, S, Hkv, D]")
+        S = k_new.shape[1]
+    if out is None:
+        out = torch.empty_like(q)
+    else:
+        _require(out.shape == q.shape and out.dtype == torch.bfloat16 and out.is_contiguous()
+                 and out.device == dev, "out must be a contiguous bf16 tensor shaped like q")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    ws_bytes = _workspace_bytes(workspace, dev)
+    with torch.cuda.device(dev):
+        st = _lib.load().mx_paged_gqa_decode_append(
+            _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache), _ptr(out),
+            _ptr(seq_lens), _ptr(block_table), B, SQ, S, Hq, Hkv, D, P, num_pages,
+            block_table.shape[1], max_seq_len, int(bool(causal)), float(scale), num_splits,
+            _ptr(workspace), ws_bytes, _stream_handle(stream, dev))
+    _lib.check(st)
+    return out
+
+
 def read_device_status(workspace: torch.Tensor | None = None, reset: bool = True,
                        stream=None, device=None) -> int:
     """Sticky MX_DEVICE_* bits raised by the kernels (synchronises the stream)."""

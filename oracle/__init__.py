@@ -23,6 +23,10 @@ Pinning (what each function is checked against, in tests/test_oracle.py):
                           scipy.special.logsumexp and the closed form log(L) (zero keys), the
                           merge of any page sharding pinned by equality with the unsharded
                           decode (itself pinned by SDPA), including causal multi-token shards.
+  paged_decode_append_reference
+                          append then decode over the L + S keys (flash_attn_with_kvcache with
+                          k / v); pinned by torch SDPA with an explicit end-aligned causal mask
+                          over the independently concatenated keys.
   paged_kv_append_reference
                           the paged K/V append (flash_attn_with_kvcache's k / v); pinned by
                           the round trip through the decode oracle against plain attention
@@ -36,6 +40,7 @@ from .paged_attention import (  # noqa: F401
     combine_partials,
     kv_bytes,
     lse_merge_reference,
+    paged_decode_append_reference,
     paged_decode_fp64,
     paged_decode_partial_reference,
     paged_decode_reference,

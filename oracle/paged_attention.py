@@ -267,3 +267,17 @@ def lse_merge_reference(o_parts, lse_parts) -> np.ndarray:
     num = (w[..., None] * o).sum(0)
     den = w.sum(0)
     return np.where(seen[..., None], num / np.where(seen, den, 1.0)[..., None], 0.0)
+
+
+def paged_decode_append_reference(q, k_new, v_new, k_cache, v_cache, block_table, seq_lens,
+                                  scale=None, causal: bool = False):
+    """Append-and-attend (flash_attn_with_kvcache with k / v given): the append of
+    ``paged_kv_append_reference``, then ``paged_decode_reference`` over max(L_b, 0) + S keys.
+    Returns (out fp32 of q's shape, k_cache, v_cache, flags); meaningful when no flag is
+    raised (every new token found a slot)."""
+    k2, v2, flags = paged_kv_append_reference(k_new, v_new, k_cache, v_cache, block_table,
+                                              seq_lens)
+    S = k_new.shape[1] if k_new.dim() == 4 else 1
+    lens = torch.as_tensor(seq_lens).cpu().to(torch.int32).clamp(min=0) + S
+    out = paged_decode_reference(q, k2, v2, block_table, lens, scale, causal=causal)
+    return out, k2, v2, flags

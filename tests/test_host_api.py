@@ -401,3 +401,37 @@ def test_balanced_schedule_bounds_its_32_bit_chunk_line():
     assert e.value.status == _lib.MX_STATUS_UNSUPPORTED
     # the same batch with a 64K-token capacity stays balanced
     assert plan(512, 16, 16, 128, 256, 16384, 65536, 0, num_cus=256)["schedule"] == "balanced"
+
+
+# ------------------------------------------------------------------------------------------
+# Append-and-attend: validation (no HIP call is reached on these paths)
+# ------------------------------------------------------------------------------------------
+
+def _decode_append(**over):
+    a = dict(q=FAKE, kn=FAKE, vn=FAKE, k=FAKE, v=FAKE, out=FAKE, lens=FAKE, table=FAKE, B=2,
+             SQ=1, S=1, Hq=32, Hkv=8, D=128, P=16, pages=64, max_pages=32, max_seq=0, causal=0,
+             scale=0.088, ns=2, ws=FAKE, ws_bytes=1 << 30, stream=None)
+    a.update(over)
+    return _lib.load().mx_paged_gqa_decode_append(
+        a["q"], a["kn"], a["vn"], a["k"], a["v"], a["out"], a["lens"], a["table"], a["B"],
+        a["SQ"], a["S"], a["Hq"], a["Hkv"], a["D"], a["P"], a["pages"], a["max_pages"],
+        a["max_seq"], a["causal"], a["scale"], a["ns"], a["ws"], a["ws_bytes"], a["stream"])
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(q=None), _lib.MX_STATUS_NULL_POINTER),
+    (dict(out=None), _lib.MX_STATUS_NULL_POINTER),
+    (dict(kn=None), _lib.MX_STATUS_NULL_POINTER),
+    (dict(table=None), _lib.MX_STATUS_NULL_POINTER),
+    (dict(vn=ctypes.c_void_p(0x1008)), _lib.MX_STATUS_INVALID_ARGUMENT),
+    (dict(q=ctypes.c_void_p(0x1008)), _lib.MX_STATUS_INVALID_ARGUMENT),
+    (dict(pages=0), _lib.MX_STATUS_INVALID_SHAPE),          # the pool bounds every write
+    (dict(S=-1), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(Hq=30), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(D=96), _lib.MX_STATUS_UNSUPPORTED),
+    (dict(causal=3), _lib.MX_STATUS_INVALID_ARGUMENT),
+    (dict(ws_bytes=100), _lib.MX_STATUS_WORKSPACE_TOO_SMALL),
+])
+def test_append_and_attend_rejects_invalid_arguments(over, status):
+    assert _decode_append(**over) == status
+    assert _lib.load().mx_last_error()

@@ -557,3 +557,34 @@ def test_planted_causal_on_every_shard_is_caught():
     exp = paged_decode_fp64(inp.q, inp.k_cache, inp.v_cache, inp.block_table, inp.seq_lens,
                             inp.scale, causal=True)
     assert np.abs(got - exp).max() > 1e-3
+
+
+@pytest.mark.parametrize("sq,causal", [(1, False), (3, True), (3, False)])
+def test_append_and_attend_is_masked_attention_over_the_concatenated_keys(sq, causal):
+    """The fused reference (append S new tokens, decode their sq queries over L + S keys) equals
+    torch SDPA over [old rows; new rows] with an explicit end-aligned mask: query token i sees
+    keys t < L + S - sq + i + 1."""
+    from oracle import paged_decode_append_reference
+    lens = [0, 4, 15, 16, 40]
+    S = 3
+    k, v, table, kn, vn, lens_t, k2, v2, flags = _append_case(lens, S, seed=12)
+    Hq, Hkv, D, P = 8, 4, 32, 16
+    g = torch.Generator().manual_seed(13)
+    q = torch.randn(len(lens), sq, Hq, D, generator=g).to(torch.bfloat16)
+    out, k3, v3, fl = paged_decode_append_reference(q, kn, vn, k, v, table, lens_t,
+                                                    1 / math.sqrt(D), causal=causal)
+    assert not fl and torch.equal(k3, k2) and torch.equal(v3, v2)
+    for b, L in enumerate(lens):
+        old_k = torch.stack([k[int(table[b, t // P]), t % P] for t in range(L)]) if L else \
+            torch.zeros(0, Hkv, D, dtype=torch.bfloat16)
+        old_v = torch.stack([v[int(table[b, t // P]), t % P] for t in range(L)]) if L else \
+            torch.zeros(0, Hkv, D, dtype=torch.bfloat16)
+        kk = torch.cat([old_k, kn[b]]).double().permute(1, 0, 2).repeat_interleave(Hq // Hkv, 0)
+        vv = torch.cat([old_v, vn[b]]).double().permute(1, 0, 2).repeat_interleave(Hq // Hkv, 0)
+        n = L + S
+        mask = torch.ones(sq, n, dtype=torch.bool)
+        if causal:
+            mask = torch.arange(n)[None, :] < (n - sq + torch.arange(sq)[:, None] + 1)
+        exp = F.scaled_dot_product_attention(q[b].double().permute(1, 0, 2), kk, vv,
+                                             attn_mask=mask)          # [Hq, sq, D]
+        assert torch.allclose(out[b].double(), exp.permute(1, 0, 2), atol=1e-5), b
