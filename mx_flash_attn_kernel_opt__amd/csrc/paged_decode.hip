@@ -150,7 +150,7 @@ constexpr bool k_via_lds() {
   return (D == 64 ? MX_K_VIA_LDS_D64 : (D == 128 ? MX_K_VIA_LDS_D128 : MX_K_VIA_LDS_D256)) != 0;
 }
 
-// Waves per workgroup of the split-KV kernel.
+// Waves per workgroup of the main kernels (split grid and balanced schedule).
 template <int D>
 constexpr int waves_per_group() {
   return D == 64 ? MX_NW_D64 : (D == 128 ? MX_NW_D128 : MX_NW_D256);
