@@ -22,7 +22,7 @@
  * padding entries after them are never touched (reference task.md:8-10, 61, 92).
  *
  * Supported shapes: head_dim in {64, 128, 256}; page_size in {16, 32, 64, 128, 256};
- * num_heads % num_kv_heads == 0 and num_heads / num_kv_heads <= 16; seqlen_q >= 1 with
+ * num_heads % num_kv_heads == 0 and num_heads / num_kv_heads <= 128; seqlen_q >= 1 with
  * batch * seqlen_q <= 65535; causal 0 or 1.  The seqlen_q * (num_heads / num_kv_heads) query
  * rows of one KV head are processed in groups of 16 rows (32 when there are more than 16 and
  * head_dim <= 128): every further group streams that head's K/V once more.

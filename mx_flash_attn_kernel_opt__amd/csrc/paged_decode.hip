@@ -1388,6 +1388,9 @@ int64_t align_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 constexpr int64_t kMinTokensPerSplit = 128;   // amortises Q load, pipeline fill and partials
 constexpr int64_t kMaxTokensPerSplit = 16384;  // bounds one workgroup's share of a sequence
 constexpr int64_t kMaxGridDim = 65535;
+// Query heads per KV head (MQA included).  Rows of one KV head are processed in 16- or 32-row
+// groups whatever the group size, so the limit only bounds how often K/V is re-streamed.
+constexpr int64_t kMaxGroup = 128;
 constexpr int64_t kBalancedMinUnits = 64;
 constexpr int64_t kBalancedMinCap = 2048;  // tokens of capacity (max_seq_len) for balanced
 constexpr int64_t kFusedMaxSplits = 16;  // split grid: merge in-kernel up to this many splits
@@ -1457,8 +1460,8 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
                 "max_pages_per_seq must all be >= 1");
   if (num_heads % num_kv_heads != 0)
     return fail(MX_STATUS_INVALID_SHAPE, "num_heads must be a multiple of num_kv_heads");
-  if (num_heads / num_kv_heads > 16)
-    return fail(MX_STATUS_UNSUPPORTED, "query group (num_heads / num_kv_heads) must be <= 16");
+  if (num_heads / num_kv_heads > kMaxGroup)
+    return fail(MX_STATUS_UNSUPPORTED, "query group (num_heads / num_kv_heads) must be <= 128");
   if (head_dim != 64 && head_dim != 128 && head_dim != 256)
     return fail(MX_STATUS_UNSUPPORTED, "head_dim must be 64, 128 or 256");
   if (page_size != 16 && page_size != 32 && page_size != 64 && page_size != 128 &&

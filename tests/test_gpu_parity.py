@@ -480,3 +480,24 @@ def test_split_grid_with_more_units_than_counters_uses_the_combine_kernel():
     inp = W.make_inputs(spec, seed=22, device=DEV)
     out = _decode(inp, num_splits=2)
     _check(inp, out, batches=_sample(B, 40), label="many units, split 2")
+
+
+# ------------------------------------------------------------------------------------------
+# Query groups above 16 (MQA-style: up to 128 query heads per KV head)
+# ------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("ns", [0, 1, 5, -9])
+@pytest.mark.parametrize("G,Hkv,D", [(24, 2, 128), (32, 1, 128), (48, 1, 64), (64, 2, 128),
+                                     (128, 1, 128), (32, 2, 256), (40, 1, 256)])
+@pytest.mark.parametrize("sq,causal", [(1, False), (2, True)])
+def test_large_query_groups(G, Hkv, D, ns, sq, causal):
+    """A group's rows run in 16- or 32-row groups like any other rows (G=32 at D<=128 is one
+    two-tile group, so K/V is streamed once); every schedule, with causal two-token queries."""
+    spec = W.custom_spec("bigG", [1, 15, 17, 300, 2049, 0], G * Hkv, Hkv, D, 16, seqlen_q=sq)
+    inp = W.make_inputs(spec, seed=G + D + sq, device=DEV)
+    out = _decode(inp, causal=causal, num_splits=ns)
+    ref = paged_decode_reference(inp.q.cpu(), inp.k_cache.cpu(), inp.v_cache.cpu(),
+                                 inp.block_table.cpu(), inp.seq_lens.cpu(), inp.scale,
+                                 causal=causal)
+    assert_close_to_oracle(out.cpu(), ref, f"G={G} Hkv={Hkv} D={D} ns={ns} sq={sq}")
+    assert read_device_status() == 0

@@ -98,7 +98,7 @@ def test_null_pointers_are_rejected(field):
     (dict(D=512), _lib.MX_STATUS_UNSUPPORTED),
     (dict(P=8), _lib.MX_STATUS_UNSUPPORTED),
     (dict(P=48), _lib.MX_STATUS_UNSUPPORTED),
-    (dict(Hq=64, Hkv=2), _lib.MX_STATUS_UNSUPPORTED),     # group 32 > 16
+    (dict(Hq=512, Hkv=2), _lib.MX_STATUS_UNSUPPORTED),    # group 256 > 128
     (dict(B=70000), _lib.MX_STATUS_UNSUPPORTED),
     (dict(SQ=0), _lib.MX_STATUS_INVALID_SHAPE),
     (dict(B=300, SQ=300), _lib.MX_STATUS_UNSUPPORTED),    # combine grid: batch * seqlen_q
