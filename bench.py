@@ -241,6 +241,87 @@ def time_append(spec: W.DecodeSpec, steps: int, warmup: int, seed: int = 0) -> d
             "note": "launch-bound: one token per sequence moves bytes_per_call"}
 
 
+def time_append_attend(spec: W.DecodeSpec, steps: int, warmup: int, seed: int = 0) -> dict:
+    """One serving step of `spec` with its newest token not yet in the cache: the cache holds
+    L - 1 tokens and the step appends token L - 1 and attends over all L.  Timed three ways on
+    rotated K/V pools (as the decode line, so every call reads its pages from HBM): the
+    one-launch mx_paged_gqa_decode_append, the append kernel followed by the decode, and the
+    decode alone over L cached tokens (the bound the other two approach)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    B, Hq, Hkv, D, P = (spec.batch, spec.num_heads, spec.num_kv_heads, spec.head_dim,
+                        spec.page_size)
+    inp = W.make_inputs(spec, seed=seed, device="cuda")
+    nbytes = inp.kv_bytes()
+    copies = (1 if nbytes >= 3 * MALL_BYTES
+              else min(MAX_POOL_COPIES, max(2, math.ceil(3 * MALL_BYTES / max(nbytes, 1)))))
+    pools = [(inp.k_cache, inp.v_cache)] + [(inp.k_cache.clone(), inp.v_cache.clone())
+                                            for _ in range(copies - 1)]
+    full = inp.seq_lens
+    cached = (full - 1).clamp(min=0)
+    kn = torch.randn(B, 1, Hkv, D, generator=g, device="cuda").to(torch.bfloat16)
+    vn = torch.randn(B, 1, Hkv, D, generator=g, device="cuda").to(torch.bfloat16)
+    plan = pkg.plan(B, Hq, Hkv, D, P, spec.max_pages, 0, 0)
+    ws = pkg.make_workspace(plan["workspace_bytes"], "cuda")
+    out = torch.empty_like(inp.q)
+    stream = torch.cuda.current_stream()
+    lib = _lib.load()
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())
+    shape = [B, 1, Hq, Hkv, D, P, inp.k_cache.shape[0], spec.max_pages, 0, 0,
+             ctypes.c_float(inp.scale), 0, vp(ws), ws.numel()]
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    # the tensor entry points validate the arguments once; the timed calls use C arguments
+    pkg.paged_gqa_decode_append(inp.q, kn, vn, inp.k_cache, inp.v_cache, inp.block_table,
+                                cached, inp.scale, out=out, workspace=ws)
+
+    def one(k, v):
+        return lib.mx_paged_gqa_decode_append(vp(inp.q), vp(kn), vp(vn), vp(k), vp(v), vp(out),
+                                              vp(cached), vp(inp.block_table), B, 1, 1, Hq,
+                                              Hkv, D, P, inp.k_cache.shape[0], spec.max_pages,
+                                              0, 0, ctypes.c_float(inp.scale), 0, vp(ws),
+                                              ws.numel(), sp)
+
+    def decode(k, v):
+        return lib.mx_paged_gqa_decode(vp(inp.q), vp(k), vp(v), vp(out), vp(full),
+                                       vp(inp.block_table), *shape, _lib.MX_PHASE_ALL, sp)
+
+    def two(k, v):
+        st = lib.mx_paged_kv_append(vp(kn), vp(vn), vp(k), vp(v), vp(cached),
+                                    vp(inp.block_table), B, 1, Hkv, D, P, inp.k_cache.shape[0],
+                                    spec.max_pages, vp(ws), sp)
+        return st or decode(k, v)
+
+    res = {}
+    # Three rounds over the three ways, the best round of each kept: the order of the ways
+    # then does not favour one (clock ramps, the pool's first touch).
+    for _ in range(3):
+        for name, fn in (("decode_only", decode), ("one_launch", one),
+                         ("append_then_decode", two)):
+            for i in range(warmup):
+                _lib.check(fn(*pools[i % copies]))
+            torch.cuda.synchronize()
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            for i in range(steps):
+                _lib.check(fn(*pools[i % copies]))
+            end.record(stream)
+            torch.cuda.synchronize()
+            us = round(start.elapsed_time(end) * 1e3 / steps, 2)
+            res[name] = min(res.get(name, us), us)
+    if pkg.read_device_status(ws):
+        raise RuntimeError("device status flags raised during the append-and-attend benchmark")
+    del inp, pools
+    torch.cuda.empty_cache()
+    return {"metric": "decode_step_with_append_us_per_call", "value": res["one_launch"],
+            "unit": "us", "higher_is_better": False, "steps": steps, "dtype": "bf16",
+            "config": {"workload": f"append_attend_{spec.name}", "batch": B, "seqlen_new": 1,
+                       "num_heads": Hq, "num_kv_heads": Hkv, "head_dim": D, "page_size": P,
+                       "schedule": plan["schedule"], "pools": copies},
+            "append_then_decode_us": res["append_then_decode"],
+            "decode_only_us": res["decode_only"],
+            "note": "value: one launch appends the new token and attends over L keys"}
+
+
 def time_shards(inp: W.DecodeInputs, num_shards: int, steps: int, warmup: int) -> dict:
     """The per-GPU pieces of a sharded decode of `inp`, all run on this one GPU: each shard's
     partial decode (shard_pages layout; calls rotate over the shards so no shard is served
@@ -567,6 +648,9 @@ def main(argv=None) -> int:
             print(lines[-1], flush=True)
         print(json.dumps(time_append(W.get_spec(W.BENCH_DEFAULT), 200, 20, args.seed)),
               flush=True)
+        for name in ("tiny", W.BENCH_DEFAULT):
+            print(json.dumps(time_append_attend(W.get_spec(name), 200, 20, args.seed)),
+                  flush=True)
     print(json.dumps(line), flush=True)
     return 0
 

@@ -216,14 +216,20 @@ int mx_paged_kv_append(const void* k_new, const void* v_new, void* k_cache, void
  * Append-and-attend: the step flash_attn_with_kvcache performs when given k / v (the
  * reference's oracle, called with k = v = None by its harness, verify_real.py:40-41).  Writes
  * k_new / v_new [batch, seqlen_new, num_kv_heads, head_dim] bf16 at positions
- * max(seq_lens[b], 0) + j of each sequence's block-table row (as mx_paged_kv_append), then
+ * max(seq_lens[b], 0) + j of each sequence's block-table row (as mx_paged_kv_append), and
  * decodes q over the max(seq_lens[b], 0) + seqlen_new keys of each sequence (with causal = 1,
  * query token i of seqlen_q sees keys t < L_new - seqlen_q + i + 1, L_new the count after the
  * append).  seq_lens are the lengths BEFORE the append and are not modified.  Other arguments
  * as mx_paged_gqa_decode (max_seq_len is the capacity after the append) and
  * mx_paged_kv_append (num_pages is required; slots past the table row or outside the pool are
- * skipped and flagged, and those keys are not attended).  The workspace is the decode's
- * (mx_paged_gqa_decode_workspace_size).  Nothing is launched on error.  Returns MX_STATUS_*.
+ * skipped and flagged, and the output of a flagged call is unspecified).  The workspace is the
+ * decode's (mx_paged_gqa_decode_workspace_size).
+ * For 1 <= seqlen_new <= 16 this is ONE launch: the new keys are read from k_new / v_new as one
+ * more chunk of each (sequence, KV head) and written to the cache by the same kernel, whose
+ * attention never reads those slots.  The pools then equal mx_paged_kv_append's bit for bit;
+ * the output differs from the two-call sequence only by summation order.  Longer appends run
+ * the append kernel, then the decode (bit-identical to the two calls).  Nothing is launched on
+ * error.  Returns MX_STATUS_*.
  * No counterpart in the reference's own code; the semantics are flash_attn_with_kvcache's.
  */
 int mx_paged_gqa_decode_append(const void* q, const void* k_new, const void* v_new,

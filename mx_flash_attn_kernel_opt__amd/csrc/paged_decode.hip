@@ -407,6 +407,15 @@ struct MainShape {
   // (written by the append kernel just before), so sequence b has max(seq_lens[b], 0) + appended
   // keys.  0 = seq_lens are the key counts.
   int appended;
+  // Append-and-attend in one launch (new_tokens = S in 1..16, else 0): the S new keys of each
+  // sequence are read from k_new / v_new [B, S, Hkv, D] as one extra masked chunk, attached to
+  // the schedule slot of the unit's last cache chunk (chunk 0 for an empty cache), and written to
+  // their cache slots at positions L + j (k_dst / v_dst) by the wave that loads them.
+  const uint16_t* k_new;
+  const uint16_t* v_new;
+  uint16_t* k_dst;
+  uint16_t* v_dst;
+  int new_tokens;
 };
 
 // Keys of sequence b before clamping (see MainShape::appended).
@@ -468,7 +477,20 @@ __device__ __forceinline__ void load_q(bf16x8 (&qop)[D / 32], const uint16_t* q,
 // tokens; chunks from c_mask on (at least the last one) are processed with masks: tokens past
 // the sequence end, and with kCausal, for this lane's query row of tile t, the keys at or past
 // row_lim[t].  Without kCausal c_mask is the last chunk and row_lim is ignored.
-template <int D, int NBUF, int NW, bool kCausal, int KT>
+// A stream_chunks hook that does nothing (see NewTokens for the one that does).
+struct NoExtraChunk {
+  template <int D>
+  __device__ __forceinline__ void load(Chunk<D>&) const {}
+  template <int D, int KT>
+  __device__ __forceinline__ void process(SoftmaxState<D> (&)[KT], const Chunk<D>&,
+                                          const bf16x8 (&)[KT][D / 32], const int (&)[KT],
+                                          char*) const {}
+  template <int D, int KT>
+  __device__ __forceinline__ void finish(SoftmaxState<D> (&)[KT], const bf16x8 (&)[KT][D / 32],
+                                         const int (&)[KT], char*) const {}
+};
+
+template <int D, int NBUF, int NW, bool kCausal, int KT, class Extra = NoExtraChunk>
 __device__ __forceinline__ void stream_chunks(SoftmaxState<D> (&st)[KT],
                                               const bf16x8 (&qop)[KT][D / 32],
                                               const uint16_t* __restrict__ kc,
@@ -476,7 +498,8 @@ __device__ __forceinline__ void stream_chunks(SoftmaxState<D> (&st)[KT],
                                               const int32_t* __restrict__ bt_row, int kv,
                                               int c_lo, int c_hi, int seq, int c_mask,
                                               const int (&row_lim)[KT], int wv, char* klds,
-                                              const MainShape& sh, bool& bad_page) {
+                                              const MainShape& sh, bool& bad_page,
+                                              const Extra& hook = Extra{}) {
   constexpr int VW = D / 16;
   const int lane = threadIdx.x & 63;
   const int r16 = lane & 15;
@@ -516,6 +539,11 @@ __device__ __forceinline__ void stream_chunks(SoftmaxState<D> (&st)[KT],
 
   Chunk<D> buf[NBUF];
   auto load = [&](Chunk<D>& dst, int64_t base) { load_chunk<D>(dst, kc + base, vc + base, lo); };
+  // The hook's extra chunk is loaded before the ring's first chunks and processed once they
+  // are in flight, so its memory latency overlaps theirs (or, where registers are short, all
+  // of it runs in hook.finish after the ring).
+  Chunk<D> xc;
+  hook.load(xc);
 
   // Register ring of NBUF chunks.  The steady-state loops process NBUF chunks and refill their
   // buffers with the next NBUF, with no conditional loads (so the compiler's vmcnt waits stay
@@ -525,6 +553,7 @@ __device__ __forceinline__ void stream_chunks(SoftmaxState<D> (&st)[KT],
   if (n >= NBUF) {
 #pragma unroll
     for (int i = 0; i < NBUF; ++i) load(buf[i], chunk_base(gc(i)));
+    hook.process(st, xc, qop, row_lim, klds);
     int k = 0;
     while (k + 2 * NBUF <= n && (!kCausal || gc(k + NBUF - 1) < c_mask)) {
       int64_t nb[NBUF];
@@ -569,10 +598,12 @@ __device__ __forceinline__ void stream_chunks(SoftmaxState<D> (&st)[KT],
 #pragma unroll
     for (int i = 0; i < NBUF; ++i)
       if (i < n) load(buf[i], chunk_base(gc(i)));
+    hook.process(st, xc, qop, row_lim, klds);
 #pragma unroll
     for (int i = 0; i < NBUF; ++i)
       if (i < n) masked(buf[i], i);
   }
+  hook.finish(st, qop, row_lim, klds);
 }
 
 // Workgroup LDS: the per-wave K transpose tiles while streaming, then (after a barrier) the
@@ -683,6 +714,225 @@ __device__ __forceinline__ void setup_row_group(bf16x8 (&qop)[KT][D / 32],
   }
 }
 
+// Extent of sequence b as the kernels see it.  keys: keys attended; cache: keys read from the
+// paged cache; sched: tokens the schedules (splits, balanced positions) cover; at: cache position
+// of the first new key (fused append only).  Without a fused append keys, cache and sched are
+// the clamped key count.  With one (MainShape::new_tokens = S) the cache holds
+// min(max(L, 0), cap) old keys and the S new ones come from k_new (L + S above the capacity is
+// flagged); an empty cache still takes one schedule slot so the unit exists.
+struct SeqExtent {
+  int keys;
+  int cache;
+  int sched;
+  int at;
+};
+template <bool kAppend>
+__device__ __forceinline__ SeqExtent seq_extent(const int32_t* seq_lens, int b,
+                                                const MainShape& sh, uint32_t* status,
+                                                bool report) {
+  if constexpr (!kAppend) {
+    const int s = clamped_len(seq_lens, b, sh, status, report);
+    return SeqExtent{s, s, s, 0};
+  }
+  const int at = max(seq_lens[b], 0);
+  if (at > sh.cap_tokens - sh.new_tokens && report)
+    atomicOr(status, (uint32_t)MX_DEVICE_SEQ_TOO_LONG);
+  const int c = min(at, sh.cap_tokens);
+  return SeqExtent{c + sh.new_tokens, c, max(c, 1), at};
+}
+
+// The fused append's extra chunk of unit (b, kv), a stream_chunks hook: in the wave that owns
+// it (`active`), load() reads the S = sh.new_tokens new rows of KV head kv from k_new / v_new
+// (rows past S re-read row S-1, so nothing past them is touched) and process() runs them as a
+// masked chunk at attended positions `cache` + j: query row r of tile t sees new key j when
+// cache + j < row_lim[t].  With `write` (one unit per KV head), process() first stores the
+// rows to their cache slots at positions at + j, like the append kernel: positions past the
+// table row and page ids outside the pool are skipped and flagged.  Those stores are issued at
+// the start of the wave's streaming, so they complete long before its next barrier, and no
+// slot written is read unmasked by the launch (cache chunks cover positions below `cache`).
+// With head_dim 256 the chunk runs after the ring instead and the cache is written by
+// copy_new_tokens at the end of the launch.
+struct NewTokens {
+  const MainShape& sh;
+  int b, kv, cache;
+  bool active;                  // wave-uniform
+  bool write;                   // wave-uniform
+  int at;                       // cache position of new row 0: max(seq_lens[b], 0)
+  const int32_t* bt_row;
+  uint32_t* status;
+
+  // With head_dim 256 the ring leaves no registers for a chunk in flight beside it: the new
+  // keys are then loaded and processed after the ring (finish).
+  template <int D>
+  static constexpr bool kOverlap = D <= 128;
+
+  template <int D>
+  __device__ __forceinline__ void load(Chunk<D>& c) const {
+    if constexpr (kOverlap<D>)
+      if (active) load_rows(c);
+  }
+  template <int D, int KT>
+  __device__ __forceinline__ void process(SoftmaxState<D> (&st)[KT], const Chunk<D>& c,
+                                          const bf16x8 (&qop)[KT][D / 32],
+                                          const int (&row_lim)[KT], char* klds) const {
+    if constexpr (kOverlap<D>) {
+      if (active) {
+        if (write) store_rows(c);
+        run(st, c, qop, row_lim, klds);
+      }
+    }
+  }
+  template <int D, int KT>
+  __device__ __forceinline__ void finish(SoftmaxState<D> (&st)[KT],
+                                         const bf16x8 (&qop)[KT][D / 32],
+                                         const int (&row_lim)[KT], char* klds) const {
+    if constexpr (!kOverlap<D>) {
+      if (active) {
+        Chunk<D> c;
+        load_rows(c);
+        run(st, c, qop, row_lim, klds);
+      }
+    }
+  }
+
+  template <int D>
+  __device__ __forceinline__ void load_rows(Chunk<D>& c) const {
+    static_assert(k_via_lds<D>(), "the fused append loads K in the LDS-staged layout");
+    // An opaque copy of the lane index: keeps the per-lane offsets of this rarely taken block
+    // from being hoisted out of the callers' loops, where they would stay live (and spill)
+    // across the streaming of every chunk.
+    int lane = threadIdx.x & 63;
+    asm volatile("" : "+v"(lane));
+    constexpr int SPR = D / 8;     // 16-byte segments per K row
+    constexpr int RPI = 64 / SPR;  // K rows per load instruction
+    constexpr int VW = D / 16;     // V elements per lane and row
+    const int S = sh.new_tokens;
+    const int64_t head0 = ((int64_t)b * S * sh.num_kv_heads + kv) * D;  // row 0 of head kv
+    const uint16_t* kb = sh.k_new + head0;
+    const uint16_t* vb = sh.v_new + head0;
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) {
+      const int rr = min(i * RPI + lane / SPR, S - 1);
+      c.k[i] = *reinterpret_cast<const u32x4*>(kb + (int64_t)rr * sh.token_stride +
+                                               8 * (lane % SPR));
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int rr = min(4 * (lane >> 4) + r, S - 1);
+      load_v_row<D>(c.v[r], vb + (int64_t)rr * sh.token_stride + VW * (lane & 15), 0u);
+    }
+  }
+
+  // The loaded rows (K in the LDS-staged layout: lane j holds 16-byte segment j % (D/8) of row
+  // i*(512/D) + j/(D/8); V: lane (r16, g4) holds elements (D/16)*r16 .. of row 4*g4 + r) go
+  // to their page slots.  The S <= 16 <= page_size positions span at most two pages, whose ids
+  // are two wave-uniform loads.
+  template <int D>
+  __device__ __forceinline__ void store_rows(const Chunk<D>& c) const {
+    int lane = threadIdx.x & 63;
+    asm volatile("" : "+v"(lane));
+    constexpr int SPR = D / 8;
+    constexpr int RPI = 64 / SPR;
+    constexpr int VW = D / 16;
+    const int S = sh.new_tokens;
+    const int psize = kChunk << sh.chunk_shift;
+    const int table_tokens = sh.max_pages * psize;
+    const int n_ok = max(0, min(S, table_tokens - at));  // rows whose position is in the row
+    if (n_ok < S && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_SEQ_TOO_LONG);
+    if (n_ok == 0) return;
+    const int page0 = at / psize;
+    const int pid0 = bt_row[page0];
+    const int pid1 = bt_row[(at + n_ok - 1) / psize];
+    auto valid = [&](int pid) { return pid >= 0 && (sh.num_pages <= 0 || pid < sh.num_pages); };
+    const bool ok0 = valid(pid0), ok1 = valid(pid1);
+    if (!(ok0 && ok1) && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
+    // Element offset of new row j's KV head kv, or -1 when it is not written.
+    auto slot = [&](int j) -> int64_t {
+      const int pos = at + j;
+      const bool first = pos / psize == page0;
+      if (j >= n_ok || !(first ? ok0 : ok1)) return -1;
+      return (int64_t)(first ? pid0 : pid1) * sh.page_stride +
+             (int64_t)(pos % psize) * sh.token_stride + kv * D;
+    };
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) {
+      const int64_t o = slot(i * RPI + lane / SPR);
+      if (o >= 0) *reinterpret_cast<u32x4*>(sh.k_dst + o + 8 * (lane % SPR)) = c.k[i];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t o = slot(4 * (lane >> 4) + r);
+      if (o >= 0) {
+        uint16_t* dst = sh.v_dst + o + VW * (lane & 15);
+        if constexpr (D == 64) {
+          *reinterpret_cast<u32x2*>(dst) = u32x2{c.v[r][0], c.v[r][1]};
+        } else {
+#pragma unroll
+          for (int w = 0; w < D / 32; w += 4)
+            *reinterpret_cast<u32x4*>(dst + 2 * w) =
+                u32x4{c.v[r][w], c.v[r][w + 1], c.v[r][w + 2], c.v[r][w + 3]};
+        }
+      }
+    }
+  }
+
+  template <int D, int KT>
+  __device__ __forceinline__ void run(SoftmaxState<D> (&st)[KT], const Chunk<D>& c,
+                                      const bf16x8 (&qop)[KT][D / 32], const int (&row_lim)[KT],
+                                      char* klds) const {
+    const int lane = threadIdx.x & 63;
+    const int S = sh.new_tokens;
+    int row_valid[KT];
+#pragma unroll
+    for (int t = 0; t < KT; ++t) row_valid[t] = max(0, min(S, row_lim[t] - cache));
+    process_chunk<D, true, KT>(st, c, qop, sh.scale_log2, lane >> 4, S, row_valid, klds, lane);
+  }
+};
+
+// The fused append's cache write for KV head kv of sequence b: new row j of k_new / v_new goes
+// to cache position max(seq_lens[b], 0) + j, like the append kernel (positions past the table
+// row and page ids outside the pool are skipped and flagged).  One workgroup per (sequence, KV
+// head) does it, as its last work: the stores' completion then delays no barrier or merge of
+// the launch, and none of these slots is read unmasked by it (cache chunks cover positions
+// below SeqExtent::cache only).
+template <int D>
+__device__ __forceinline__ void copy_new_tokens(const int32_t* __restrict__ seq_lens,
+                                                const int32_t* __restrict__ block_table, int b,
+                                                int kv, const MainShape& sh, uint32_t* status,
+                                                int tid, int nthreads) {
+  constexpr int SEG = D / 8;  // 16-byte segments per row of one KV head
+  const int S = sh.new_tokens;
+  const int at = max(seq_lens[b], 0);
+  const int psize = kChunk << sh.chunk_shift;
+  const int table_tokens = sh.max_pages * psize;
+  const int32_t* bt_row = block_table + (int64_t)b * sh.max_pages;
+  bool overflow = false, bad = false;
+  for (int e = tid; e < 2 * S * SEG; e += nthreads) {
+    const int is_v = e >= S * SEG;
+    const int j = (e - is_v * S * SEG) / SEG;
+    const int seg = e % SEG;
+    if (at >= table_tokens - j) {  // at + j past the table row (no int overflow)
+      overflow = true;
+      continue;
+    }
+    const int pos = at + j;
+    const int pid = bt_row[pos / psize];
+    if (pid < 0 || (sh.num_pages > 0 && pid >= sh.num_pages)) {
+      bad = true;
+      continue;
+    }
+    const int64_t src = (((int64_t)b * S + j) * sh.num_kv_heads + kv) * D + 8 * seg;
+    const int64_t dst = (int64_t)pid * sh.page_stride + (int64_t)(pos % psize) * sh.token_stride +
+                        kv * D + 8 * seg;
+    const u32x4 x = *reinterpret_cast<const u32x4*>((is_v ? sh.v_new : sh.k_new) + src);
+    *reinterpret_cast<u32x4*>((is_v ? sh.v_dst : sh.k_dst) + dst) = x;
+  }
+  if (__builtin_amdgcn_ballot_w64(overflow) != 0 && (tid & 63) == 0)
+    atomicOr(status, (uint32_t)MX_DEVICE_SEQ_TOO_LONG);
+  if (__builtin_amdgcn_ballot_w64(bad) != 0 && (tid & 63) == 0)
+    atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
+}
+
 constexpr int kMergeFanIn = 8;   // partials merged per step of a cross-workgroup merge
 
 // Cross-workgroup handoff of partials.  Device-scoped accesses (MX_MERGE_SCOPED_ACCESS = 1):
@@ -771,7 +1021,7 @@ __device__ __forceinline__ void acquire_partials() {
 // split and row.  With fused_combine the last split of each unit to finish (a device-scope
 // arrival counter per unit) merges them itself, so the whole call is one launch; otherwise
 // mx_paged_decode_combine merges them in a second launch.
-template <int D, int NBUF, int NW, bool kCausal, int KT>
+template <int D, int NBUF, int NW, bool kCausal, int KT, bool kAppend>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     KT == 2 ? 1 : (D == 64 ? MX_WAVES_PER_EU_D64 : (D == 128 ? MX_WAVES_PER_EU_D128 : MX_WAVES_PER_EU_D256)))))
 void mx_paged_decode_splitkv(
@@ -795,8 +1045,10 @@ void mx_paged_decode_splitkv(
   const int split = blockIdx.z;
   const int nrows = min(16 * KT, sh.rows - r0);  // query rows of this group
 
-  const int seq = clamped_len(seq_lens, b, sh, status, split == 0 && blockIdx.x == 0 && tid == 0);
-  if (seq <= 0) {
+  const SeqExtent ext =
+      seq_extent<kAppend>(seq_lens, b, sh, status, split == 0 && blockIdx.x == 0 && tid == 0);
+  const int seq = ext.sched;
+  if (ext.keys <= 0) {
     // Empty sequence: defined as a zero output.
     if (split == 0)
       for (int e = tid; e < nrows * (D / 4); e += 64 * NW)
@@ -808,20 +1060,42 @@ void mx_paged_decode_splitkv(
   if (t0 >= seq) return;  // uniform over the workgroup: no barrier is skipped by part of it
   const int t1 = min(t0 + sh.tokens_per_split, seq);
   const bool single = seq <= sh.tokens_per_split;
-  const int c_last = (seq - 1) / kChunk;
-  // First chunk any row of this group must mask (causal), else the last chunk.
+  const int n_cache = (ext.cache + kChunk - 1) / kChunk;  // chunks read from the paged cache
+  const int c_lo = t0 / kChunk;
+  const int c_hi = (t1 + kChunk - 1) / kChunk;
+  // First chunk any row of this group must mask (causal), else the last cache chunk.
   const int c_mask =
-      kCausal ? min(c_last, max(0, row_key_limit(r0, seq, sh)) / kChunk) : c_last;
+      kCausal ? min(n_cache - 1, max(0, row_key_limit(r0, ext.keys, sh)) / kChunk) : n_cache - 1;
+
+  // Fused append with head_dim 256: the workgroup of split 0 and row group 0 writes the new
+  // tokens of (b, kv) to the cache, after its share of the attention (and after its arrival at
+  // the merge).
+  auto copy_if_writer = [&]() {
+    if constexpr (kAppend && !NewTokens::kOverlap<D>)
+      if (split == 0 && grp == 0)
+        copy_new_tokens<D>(seq_lens, block_table, b, kv, sh, status, tid, 64 * NW);
+  };
 
   bf16x8 qop[KT][D / 32];
   SoftmaxState<D> st[KT];
   int row_lim[KT];
-  setup_row_group<D, KT>(qop, st, row_lim, q, b, kv, grp, seq, sh, lane);
+  setup_row_group<D, KT>(qop, st, row_lim, q, b, kv, grp, ext.keys, sh, lane);
   bool bad_page = false;
-  stream_chunks<D, NBUF, NW, kCausal, KT>(st, qop, kc, vc,
-                                          block_table + (int64_t)b * sh.max_pages, kv,
-                                          t0 / kChunk, (t1 + kChunk - 1) / kChunk, seq, c_mask,
-                                          row_lim, wv, L::ktile(lds, wv), sh, bad_page);
+  const int32_t* bt_row = block_table + (int64_t)b * sh.max_pages;
+  const int c_end = min(c_hi, n_cache);
+  if constexpr (kAppend) {
+    // Fused append: the split holding the last schedule chunk also takes the new keys, as one
+    // more chunk after its cache chunks in the waves' round-robin order.
+    const bool last = c_hi * kChunk >= seq;
+    const NewTokens nt{sh,          b,          kv,    ext.cache, last && wv == (c_end - c_lo) % NW,
+                       grp == 0,    ext.at,     bt_row, status};
+    stream_chunks<D, NBUF, NW, kCausal, KT>(st, qop, kc, vc, bt_row, kv, c_lo, c_end, ext.cache,
+                                            c_mask, row_lim, wv, L::ktile(lds, wv), sh, bad_page,
+                                            nt);
+  } else {
+    stream_chunks<D, NBUF, NW, kCausal, KT>(st, qop, kc, vc, bt_row, kv, c_lo, c_end, ext.cache,
+                                            c_mask, row_lim, wv, L::ktile(lds, wv), sh, bad_page);
+  }
   if (bad_page && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
   publish_wave_state<D, NW, KT>(lds, st, wv);
   for (int e = tid; e < nrows * (D / 4); e += 64 * NW) {
@@ -840,7 +1114,10 @@ void mx_paged_decode_splitkv(
       if (d == 0) part_lse[row * sh.num_splits + split] = lse;
     }
   }
-  if (single || !sh.fused_combine) return;
+  if (single || !sh.fused_combine) {
+    copy_if_writer();
+    return;
+  }
 
   // Arrival of this split; the unit's last split merges all of them.
   const int nsv = (seq + sh.tokens_per_split - 1) / sh.tokens_per_split;  // splits with tokens
@@ -849,7 +1126,10 @@ void mx_paged_decode_splitkv(
   __syncthreads();
   if (tid == 0) s_last = (atomicAdd(counter, 1u) == (uint32_t)(nsv - 1)) ? 1 : 0;
   __syncthreads();
-  if (!s_last) return;
+  if (!s_last) {
+    copy_if_writer();
+    return;
+  }
   if (tid == 0) *counter = 0u;  // ready for the next call
   acquire_partials();
   // out[row] = sum_s 2^(lse_s - M) O_s / sum_s 2^(lse_s - M), M = max_s lse_s; a causal row no
@@ -896,6 +1176,7 @@ void mx_paged_decode_splitkv(
     store_row4<D>(out, sh, row, d, acc * (seen ? 1.0f / wsum : 0.f),
                   seen ? mx + log2f(wsum) : -INFINITY);
   }
+  copy_if_writer();
 }
 
 // ------------------------------------------------------------------------------------------
@@ -927,7 +1208,7 @@ __device__ __forceinline__ int block_sum(int x, int* sred) {
 // entirely is written out as bf16; a unit cut into several pieces has each piece written as
 // a normalised partial (O/l, log2-sum-exp) to its own slot, and the last piece to finish
 // merges them through a fan-in-8 tree of per-unit counters, so the whole call is one launch.
-template <int D, int NBUF, int NW, bool kCausal, int KT>
+template <int D, int NBUF, int NW, bool kCausal, int KT, bool kAppend>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     KT == 2 ? 1 : (D == 64 ? MX_WAVES_PER_EU_D64 : (D == 128 ? MX_WAVES_PER_EU_D128 : MX_WAVES_PER_EU_D256)))))
 void mx_paged_decode_balanced(
@@ -952,7 +1233,7 @@ void mx_paged_decode_balanced(
   // Empty sequences (L <= 0) are defined as zero output; sequence b's zeros (its seqlen_q *
   // num_heads consecutive rows) are written by workgroup b % num_groups.
   for (int b = wg; b < B; b += sh.num_groups) {
-    if (key_count(seq_lens, b, sh.appended) <= 0) {
+    if (!kAppend && key_count(seq_lens, b, sh.appended) <= 0) {
       const int64_t row0 = (int64_t)b * sh.seqlen_q * sh.num_heads;
       for (int e = tid; e < sh.seqlen_q * sh.num_heads * (D / 4); e += 64 * NW)
         store_row4<D>(out, sh, row0 + e / (D / 4), 4 * (e % (D / 4)), f32x4{0.f, 0.f, 0.f, 0.f},
@@ -965,7 +1246,7 @@ void mx_paged_decode_balanced(
   // and the scan that locates this workgroup's first position.
   constexpr int kScanPerThread = (512 + 64 * NW - 1) / (64 * NW);
   auto weight = [&](int b, bool report) -> int {
-    const int seq = clamped_len(seq_lens, b, sh, status, report);
+    const int seq = seq_extent<kAppend>(seq_lens, b, sh, status, report).sched;
     return seq > 0 ? UPS * ((seq + kChunk - 1) / kChunk + alpha) : 0;
   };
   int wts[kScanPerThread];
@@ -1030,8 +1311,8 @@ void mx_paged_decode_balanced(
   int seq_start = __builtin_amdgcn_readfirstlane(s_int[NW + 1]);
   if (b < 0) return;  // unreachable: the positions of non-empty sequences tile [0, total)
 
-  int seq = clamped_len(seq_lens, b, sh, status, false);
-  int n_b = (seq + kChunk - 1) / kChunk;
+  SeqExtent ext = seq_extent<kAppend>(seq_lens, b, sh, status, false);
+  int n_b = (ext.sched + kChunk - 1) / kChunk;
   int span = n_b + alpha;
   int j = (x_begin - seq_start) / span;  // (KV head, row group) of the unit
   int u0 = seq_start + j * span;  // first position of unit (b, j)
@@ -1052,18 +1333,29 @@ void mx_paged_decode_balanced(
       const int64_t rbase = row_base(b, kv, sh);
       const int first_wg = cpos / qsz;
       const int npieces = (cpos + n_b - 1) / qsz - first_wg + 1;
-      const int c_last = n_b - 1;
-      const int c_mask =
-          kCausal ? min(c_last, max(0, row_key_limit(r0, seq, sh)) / kChunk) : c_last;
+      const int n_cache = (ext.cache + kChunk - 1) / kChunk;  // chunks read from the cache
+      const int c_mask = kCausal ? min(n_cache - 1, max(0, row_key_limit(r0, ext.keys, sh)) / kChunk)
+                                 : n_cache - 1;
 
       bf16x8 qop[KT][D / 32];
       SoftmaxState<D> st[KT];
       int row_lim[KT];
-      setup_row_group<D, KT>(qop, st, row_lim, q, b, kv, grp, seq, sh, lane);
-      stream_chunks<D, NBUF, NW, kCausal, KT>(st, qop, kc, vc,
-                                              block_table + (int64_t)b * sh.max_pages, kv, ca,
-                                              cb, seq, c_mask, row_lim, wv, L::ktile(lds, wv),
-                                              sh, bad_page);
+      setup_row_group<D, KT>(qop, st, row_lim, q, b, kv, grp, ext.keys, sh, lane);
+      const int32_t* bt_row = block_table + (int64_t)b * sh.max_pages;
+      const int c_end = min(cb, n_cache);
+      if constexpr (kAppend) {
+        // Fused append: the piece holding the unit's last schedule chunk also takes the new
+        // keys, as one more chunk after its cache chunks in the waves' round-robin order.
+        const NewTokens nt{sh,       b,      kv,     ext.cache, cb == n_b && wv == (c_end - ca) % NW,
+                           grp == 0, ext.at, bt_row, status};
+        stream_chunks<D, NBUF, NW, kCausal, KT>(st, qop, kc, vc, bt_row, kv, ca, c_end,
+                                                ext.cache, c_mask, row_lim, wv,
+                                                L::ktile(lds, wv), sh, bad_page, nt);
+      } else {
+        stream_chunks<D, NBUF, NW, kCausal, KT>(st, qop, kc, vc, bt_row, kv, ca, c_end,
+                                                ext.cache, c_mask, row_lim, wv,
+                                                L::ktile(lds, wv), sh, bad_page);
+      }
       publish_wave_state<D, NW, KT>(lds, st, wv);
 
       if (npieces == 1) {
@@ -1166,14 +1458,22 @@ void mx_paged_decode_balanced(
     if (u0 >= x_end) break;
     if (++j == UPS) {
       j = 0;
-      seq = 0;
-      while (seq <= 0 && ++b < B) seq = clamped_len(seq_lens, b, sh, status, false);
+      ext.sched = 0;
+      while (ext.sched <= 0 && ++b < B) ext = seq_extent<kAppend>(seq_lens, b, sh, status, false);
       if (b >= B) break;  // unreachable: positions only exist for non-empty sequences
-      n_b = (seq + kChunk - 1) / kChunk;
+      n_b = (ext.sched + kChunk - 1) / kChunk;
       span = n_b + alpha;
     }
   }
   if (bad_page && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
+  if constexpr (kAppend && !NewTokens::kOverlap<D>) {
+    // Fused append with head_dim 256: the cache writes of the (sequence, KV head) pairs, spread
+    // over the workgroups that hold positions, each doing its share after all its pieces.
+    const int n_active = (total + qsz - 1) / qsz;
+    for (int pr = wg; pr < B * sh.num_kv_heads; pr += n_active)
+      copy_new_tokens<D>(seq_lens, block_table, pr / sh.num_kv_heads, pr % sh.num_kv_heads, sh,
+                         status, tid, 64 * NW);
+  }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1281,12 +1581,14 @@ __global__ __launch_bounds__(64) void mx_paged_decode_combine(
     const float* __restrict__ part_o, const float* __restrict__ part_lse,
     const int32_t* __restrict__ seq_lens, uint16_t* __restrict__ out, float* __restrict__ o_out,
     float* __restrict__ lse_out, int num_heads, int seqlen_q, int num_splits,
-    int tokens_per_split, int cap_tokens, int appended) {
+    int tokens_per_split, int cap_tokens, int appended, int new_tokens) {
   const int h = blockIdx.x;
   const int bt = blockIdx.y;  // sequence * seqlen_q + query token
   const int b = bt / seqlen_q;
   const int lane = threadIdx.x;
-  const int seq = min(key_count(seq_lens, b, appended), cap_tokens);
+  // Tokens the splits cover (SeqExtent::sched of the main kernel).
+  const int seq = new_tokens > 0 ? max(min(max(seq_lens[b], 0), cap_tokens), 1)
+                                 : min(key_count(seq_lens, b, appended), cap_tokens);
   if (seq <= tokens_per_split) return;  // single split (or empty): main kernel wrote it
   const int nsv = (seq + tokens_per_split - 1) / tokens_per_split;
   const int64_t row = (int64_t)bt * num_heads + h;
@@ -1617,12 +1919,21 @@ int internal_workspace(int64_t need, void** out) {
   return MX_STATUS_OK;
 }
 
+// How a decode launch finds the newest keys of each sequence (see MainShape::appended and
+// MainShape::new_tokens).
+struct AppendArgs {
+  int appended = 0;    // already appended to the cache: seq_lens exclude them
+  int new_tokens = 0;  // fused append: read from k_new / v_new and written to the cache
+  const void* k_new = nullptr;
+  const void* v_new = nullptr;
+};
+
 template <int D, bool kCausal, int KT>
 hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v, void* out,
                   const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
                   int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads, int64_t page_size,
                   int64_t num_pages, int64_t max_pages, float scale, char* ws, int32_t phase,
-                  float* o_out, float* lse_out, int appended, hipStream_t stream) {
+                  float* o_out, float* lse_out, const AppendArgs& app, hipStream_t stream) {
   constexpr int kNW = waves_per_group<D>();
   constexpr int kNBUF = ring_depth<D>();
   MainShape sh;
@@ -1651,14 +1962,25 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   sh.num_slots = (int)plan.slots;
   sh.o_out = o_out;
   sh.lse_out = lse_out;
-  sh.appended = appended;
+  sh.appended = app.appended;
+  sh.new_tokens = app.new_tokens;
+  sh.k_new = static_cast<const uint16_t*>(app.k_new);
+  sh.v_new = static_cast<const uint16_t*>(app.v_new);
+  // The cache is written (fused append) only through the entry that takes it as mutable.
+  sh.k_dst = app.new_tokens > 0 ? static_cast<uint16_t*>(const_cast<void*>(k)) : nullptr;
+  sh.v_dst = app.new_tokens > 0 ? static_cast<uint16_t*>(const_cast<void*>(v)) : nullptr;
   uint32_t* status = reinterpret_cast<uint32_t*>(ws);
+  // The fused-append variants of the main kernels load the new keys in the LDS-staged K layout.
+  constexpr bool kCanAppend = k_via_lds<D>();
+  const bool append = app.new_tokens > 0;
+  if (append && !kCanAppend) return hipErrorInvalidValue;
 
   if (plan.schedule == MX_SCHEDULE_BALANCED) {
     // One launch does everything; MX_PHASE_COMBINE_ONLY has nothing left to do.
     if (phase == MX_PHASE_COMBINE_ONLY) return hipSuccess;
-    hipLaunchKernelGGL((mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT>),
-                       dim3((unsigned)plan.groups),
+    const auto kernel = append ? mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, kCanAppend>
+                               : mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, false>;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)plan.groups),
                        dim3(64 * kNW), 0, stream, static_cast<const uint16_t*>(q),
                        static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
                        static_cast<uint16_t*>(out), seq_lens, block_table,
@@ -1681,9 +2003,11 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   if (phase != MX_PHASE_COMBINE_ONLY) {
     const dim3 grid((unsigned)(num_kv_heads * plan.row_tiles), (unsigned)batch,
                     (unsigned)plan.splits);
-    hipLaunchKernelGGL((mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT>), grid, dim3(64 * kNW), 0,
-                       stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                       static_cast<const uint16_t*>(v), static_cast<uint16_t*>(out), seq_lens,
+    const auto kernel = append ? mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT, kCanAppend>
+                               : mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT, false>;
+    hipLaunchKernelGGL(kernel, grid, dim3(64 * kNW), 0, stream, static_cast<const uint16_t*>(q),
+                       static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+                       static_cast<uint16_t*>(out), seq_lens,
                        block_table, part_o, part_lse,
                        reinterpret_cast<uint32_t*>(ws + kStatusBytes), status, sh);
     const hipError_t e = hipGetLastError();
@@ -1694,7 +2018,7 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
     hipLaunchKernelGGL(mx_paged_decode_combine<D>, grid, dim3(64), 0, stream, part_o, part_lse,
                        seq_lens, static_cast<uint16_t*>(out), o_out, lse_out, (int)num_heads,
                        (int)seqlen_q, (int)plan.splits, (int)plan.tokens_per_split,
-                       (int)plan.cap_tokens, appended);
+                       (int)plan.cap_tokens, app.appended, app.new_tokens);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -1778,13 +2102,13 @@ int prepare_decode(const void* q, const void* k_cache, const void* v_cache, cons
 }
 
 // Launches a prepared decode: bf16 into out, or (partial outputs) fp32 rows into o_out and
-// natural-log sum-exps into lse_out (out is then null).  `appended`: see MainShape.
+// natural-log sum-exps into lse_out (out is then null).  `app`: see AppendArgs.
 int run_decode(const Plan& plan, const void* q, const void* k_cache, const void* v_cache,
                void* out, float* o_out, float* lse_out, const int32_t* seq_lens,
                const int32_t* block_table, int64_t batch, int64_t seqlen_q, int64_t num_heads,
                int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_pages,
                int64_t max_pages_per_seq, int32_t causal, float scale, void* workspace,
-               int32_t phase, int32_t appended, void* stream) {
+               int32_t phase, const AppendArgs& app, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   hipError_t e;
@@ -1793,7 +2117,7 @@ int run_decode(const Plan& plan, const void* q, const void* k_cache, const void*
 #define MX_LAUNCH(DIM, CAUSAL, KT)                                                            \
   launch<DIM, CAUSAL, KT>(plan, q, k_cache, v_cache, out, seq_lens, block_table, batch, seqlen_q, \
                       num_heads, num_kv_heads, page_size, num_pages, max_pages_per_seq, scale, \
-                      ws, phase, o_out, lse_out, appended, s)
+                      ws, phase, o_out, lse_out, app, s)
   const bool pair = plan.tiles_per_group == 2;
   switch (head_dim) {
     case 64:
@@ -1830,7 +2154,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* o
   if (st != MX_STATUS_OK) return st;
   return run_decode(plan, q, k_cache, v_cache, out, o_out, lse_out, seq_lens, block_table, batch,
                     seqlen_q, num_heads, num_kv_heads, head_dim, page_size, num_pages,
-                    max_pages_per_seq, causal, scale, workspace, phase, 0, stream);
+                    max_pages_per_seq, causal, scale, workspace, phase, AppendArgs{}, stream);
 }
 
 // Argument checks of a paged K/V append (shared by mx_paged_kv_append and the fused
@@ -2053,15 +2377,27 @@ int mx_paged_gqa_decode_append(const void* q, const void* k_new, const void* v_n
                       head_dim, page_size, num_pages, max_pages_per_seq, max_seq_len, causal,
                       scale, num_splits, &workspace, workspace_bytes, 0, &plan);
   if (st != MX_STATUS_OK) return st;
-  if (seqlen_new > 0) {
+  AppendArgs app;
+  const bool lds_k = head_dim == 64    ? k_via_lds<64>()
+                     : head_dim == 128 ? k_via_lds<128>()
+                                       : k_via_lds<256>();
+  if (seqlen_new >= 1 && seqlen_new <= kChunk && lds_k) {
+    // One launch: the new keys are one extra chunk of each unit, written to the cache by the
+    // wave that loads them.
+    app.new_tokens = (int)seqlen_new;
+    app.k_new = k_new;
+    app.v_new = v_new;
+  } else if (seqlen_new > 0) {
+    // Longer appends: the append kernel first, then the decode over seq_lens + seqlen_new.
     st = launch_append(k_new, v_new, k_cache, v_cache, seq_lens, block_table, batch, seqlen_new,
                        num_kv_heads, head_dim, page_size, num_pages, max_pages_per_seq,
                        workspace, stream);
     if (st != MX_STATUS_OK) return st;
+    app.appended = (int)seqlen_new;
   }
   return run_decode(plan, q, k_cache, v_cache, out, nullptr, nullptr, seq_lens, block_table,
                     batch, seqlen_q, num_heads, num_kv_heads, head_dim, page_size, num_pages,
-                    max_pages_per_seq, causal, scale, workspace, 0, (int32_t)seqlen_new, stream);
+                    max_pages_per_seq, causal, scale, workspace, 0, app, stream);
 }
 
 int mx_last_status(void) { return g_last_status; }

@@ -337,6 +337,9 @@ def paged_gqa_decode_append(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.T
     max(seq_lens[b], 0) + j; seq_lens are the lengths before the append and are not modified
     (add S before the next call).  q: [B, Hq, D] or [B, seqlen_q, Hq, D]; with ``causal`` query
     token i sees keys t < L + S - seqlen_q + i + 1.  Returns the bf16 output shaped like q.
+    For S <= 16 the append and the attention are one kernel launch (the new keys are read from
+    k_new / v_new as one more chunk and written to the cache by the same kernel); longer
+    appends run the append kernel first.
     """
     dev, B, SQ, Hq, D, num_pages, P, Hkv = _check_decode_inputs(q, k_cache, v_cache,
                                                                 block_table, seq_lens)

@@ -100,35 +100,108 @@ def _fused_case(lens, S, sq, P=16, Hkv=8, Hq=32, D=128, seed=0):
     return k, v, table, kn, vn, q, torch.tensor(lens, dtype=torch.int32)
 
 
-@pytest.mark.parametrize("ns", [0, 1, 4, -7])
+@pytest.mark.parametrize("ns", [0, 1, 4, 20, -7])
 @pytest.mark.parametrize("S,sq,causal", [(1, 1, False), (4, 4, True), (8, 8, True),
-                                         (3, 1, False), (5, 2, True)])
+                                         (3, 1, False), (5, 2, True), (16, 3, True),
+                                         (17, 2, True)])
 def test_append_and_attend_matches_the_oracle(S, sq, causal, ns):
     """One call appends the S new tokens and decodes the sq query tokens over L + S keys;
-    the pools are bit-exact against the oracle's append, the output within tolerance."""
+    the pools are bit-exact against the oracle's append, the output within tolerance.  S <= 16
+    runs as one launch (the new keys are an extra chunk of each unit), S = 17 as the append
+    kernel followed by the decode; ns 20 takes the split grid's separate combine kernel."""
     from mx_flash_attn_kernel_opt__amd import paged_gqa_decode_append
     from oracle import paged_decode_append_reference
-    lens = [0, 1, 15, 16, 100, 1000, 2047]
+    lens = [0, 1, 15, 16, 100, 1000, 2047, -3]
     k, v, table, kn, vn, q, lens_t = _fused_case(lens, S, sq, seed=S * 10 + sq)
     ref, k2, v2, flags = paged_decode_append_reference(q, kn, vn, k, v, table, lens_t,
                                                        causal=causal)
     assert not flags
     kd, vd, td, ld = k.to(DEV), v.to(DEV), table.to(DEV), lens_t.to(DEV)
+    label = f"append+attend S={S} sq={sq} causal={causal} ns={ns}"
+    print(label, flush=True)
     out = paged_gqa_decode_append(q.to(DEV), kn.to(DEV), vn.to(DEV), kd, vd, td, ld,
                                   causal=causal, num_splits=ns)
     torch.cuda.synchronize()
     assert torch.equal(kd.cpu(), k2) and torch.equal(vd.cpu(), v2)
     assert torch.equal(ld.cpu(), lens_t)            # lengths are not modified
-    assert_close_to_oracle(out, ref, f"append+attend S={S} sq={sq} causal={causal} ns={ns}")
+    assert_close_to_oracle(out, ref, label)
     assert read_device_status() == 0
 
 
+@pytest.mark.parametrize("ns", [0, 3, -5])
+@pytest.mark.parametrize("D,P,Hkv,G,S,sq", [
+    (64, 16, 2, 4, 6, 3),       # head_dim 64 (two waves per workgroup)
+    (128, 64, 4, 8, 2, 3),      # 24 rows: paired row tiles
+    (256, 32, 2, 4, 9, 2),      # head_dim 256 (register ring of one)
+    (128, 16, 1, 40, 5, 3),     # 120 rows: eight row groups, only the first writes the cache
+    (64, 256, 4, 2, 16, 16),    # 16 new keys, 16 query tokens, 256-token pages
+])
+def test_append_and_attend_shapes(D, P, Hkv, G, S, sq, ns):
+    from mx_flash_attn_kernel_opt__amd import paged_gqa_decode_append
+    from oracle import paged_decode_append_reference
+    lens = [0, 5, P - 1, P, 3 * P + 7, 700]
+    k, v, table, kn, vn, q, lens_t = _fused_case(lens, S, sq, P=P, Hkv=Hkv, Hq=Hkv * G, D=D,
+                                                 seed=D + P + S)
+    ref, k2, v2, flags = paged_decode_append_reference(q, kn, vn, k, v, table, lens_t,
+                                                       causal=True)
+    assert not flags
+    kd, vd = k.to(DEV), v.to(DEV)
+    label = f"append+attend D={D} P={P} Hkv={Hkv} G={G} S={S} sq={sq} ns={ns}"
+    print(label, flush=True)
+    out = paged_gqa_decode_append(q.to(DEV), kn.to(DEV), vn.to(DEV), kd, vd, table.to(DEV),
+                                  lens_t.to(DEV), causal=True, num_splits=ns)
+    torch.cuda.synchronize()
+    assert torch.equal(kd.cpu(), k2) and torch.equal(vd.cpu(), v2)
+    assert_close_to_oracle(out, ref, label)
+    assert read_device_status() == 0
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_append_and_attend_random(seed):
+    """Seeded random shapes, lengths (empty, negative, page boundaries), new-token counts
+    1..16, query tokens, causal flag and schedule."""
+    import random
+    from mx_flash_attn_kernel_opt__amd import paged_gqa_decode_append
+    from oracle import paged_decode_append_reference
+    r = random.Random(5000 + seed)
+    D = r.choice([64, 128, 256])
+    P = r.choice([16, 32, 64, 128])
+    Hkv = r.choice([1, 2, 4, 8])
+    G = r.choice([1, 2, 3, 4, 8, 16])
+    S = r.randint(1, 16)
+    sq = r.choice([1, 1, 2, 4, S])
+    B = r.randint(1, 6)
+    cap = r.choice([20, 200, 600])
+    lens = [r.choice([-2, 0, 1, 15, 16, 17, P - 1, P, r.randint(0, cap)]) for _ in range(B)]
+    causal = r.random() < 0.5
+    ns = r.choice([0, 0, 1, 2, 5, 24, -1, -3, -11])
+    k, v, table, kn, vn, q, lens_t = _fused_case(lens, S, sq, P=P, Hkv=Hkv, Hq=Hkv * G, D=D,
+                                                 seed=seed)
+    ref, k2, v2, flags = paged_decode_append_reference(q, kn, vn, k, v, table, lens_t,
+                                                       causal=causal)
+    assert not flags
+    kd, vd = k.to(DEV), v.to(DEV)
+    label = f"seed {seed}: D={D} P={P} Hkv={Hkv} G={G} S={S} sq={sq} lens={lens} " \
+            f"causal={causal} ns={ns}"
+    print(label, flush=True)
+    out = paged_gqa_decode_append(q.to(DEV), kn.to(DEV), vn.to(DEV), kd, vd, table.to(DEV),
+                                  lens_t.to(DEV), causal=causal, num_splits=ns)
+    torch.cuda.synchronize()
+    assert torch.equal(kd.cpu(), k2) and torch.equal(vd.cpu(), v2), label
+    assert_close_to_oracle(out, ref, label)
+    assert read_device_status() == 0, label
+
+
+@pytest.mark.parametrize("S", [4, 17])
 @pytest.mark.parametrize("ns", [0, 3])
-def test_append_and_attend_equals_the_two_calls(ns):
-    """Bit for bit the same as mx_paged_kv_append followed by the decode over seq_lens + S."""
+def test_append_and_attend_equals_the_two_calls(ns, S):
+    """Against mx_paged_kv_append followed by the decode over seq_lens + S: the pools bit for
+    bit; the output bit for bit where the entry runs those two launches (S = 17), within the
+    tolerance where it runs one (S = 4: the new keys form their own chunk, so the softmax sums
+    in another order)."""
     from mx_flash_attn_kernel_opt__amd import paged_gqa_decode_append
     lens = [0, 7, 64, 300, 4000]
-    S, sq = 4, 4
+    sq = 4
     k, v, table, kn, vn, q, lens_t = _fused_case(lens, S, sq, seed=21)
     kd1, vd1, kd2, vd2 = k.to(DEV), v.to(DEV), k.to(DEV), v.to(DEV)
     td, ld, qd, knd, vnd = table.to(DEV), lens_t.to(DEV), q.to(DEV), kn.to(DEV), vn.to(DEV)
@@ -137,7 +210,33 @@ def test_append_and_attend_equals_the_two_calls(ns):
     two = paged_gqa_decode(qd, kd2, vd2, td, ld + S, causal=True, num_splits=ns)
     torch.cuda.synchronize()
     assert torch.equal(kd1, kd2) and torch.equal(vd1, vd2)
-    assert torch.equal(fused, two)
+    if S > 16:
+        assert torch.equal(fused, two)
+    else:
+        assert_close_to_oracle(fused, two.float(), f"one launch vs two, ns={ns}")
+
+
+@pytest.mark.parametrize("ns", [0, 2, -3])
+def test_append_and_attend_flags_like_the_two_calls(ns):
+    """Positions past the table row and page ids outside the pool: the same writes are skipped
+    and the same status bits raised as by the append kernel and the decode."""
+    from mx_flash_attn_kernel_opt__amd import paged_gqa_decode_append
+    P, Hkv, D, S = 16, 8, 128, 4
+    k, v, table, g = _pools(2, 4, P, Hkv, D, seed=3)      # 64 slots per row
+    table[1, 0] = 9999                                    # outside the pool
+    kn = torch.randn(2, S, Hkv, D, generator=g).to(torch.bfloat16)
+    vn = torch.randn(2, S, Hkv, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(2, Hkv * 4, D, generator=g).to(torch.bfloat16)
+    lens_t = torch.tensor([62, 3], dtype=torch.int32)    # tokens 64, 65 of row 0 overflow
+    k2, v2, flags = paged_kv_append_reference(kn, vn, k, v, table, lens_t)
+    assert flags == {"seq_too_long", "bad_page"}
+    kd, vd, td, ld = k.to(DEV), v.to(DEV), table.to(DEV), lens_t.to(DEV)
+    ws = make_workspace(1 << 20, DEV)
+    paged_gqa_decode_append(q.to(DEV), kn.to(DEV), vn.to(DEV), kd, vd, td, ld, num_splits=ns,
+                            workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(kd.cpu(), k2) and torch.equal(vd.cpu(), v2)
+    assert read_device_status(ws) == _lib.MX_DEVICE_SEQ_TOO_LONG | _lib.MX_DEVICE_BAD_PAGE_ID
 
 
 def test_append_and_attend_of_zero_tokens_is_the_decode():
