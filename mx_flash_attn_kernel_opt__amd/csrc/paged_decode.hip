@@ -1220,6 +1220,7 @@ void mx_paged_decode_balanced(
   using L = GroupLds<D, NW, KT>;
   __shared__ __attribute__((aligned(16))) char lds[L::kBytes];
   __shared__ int s_int[NW + 4];
+  __shared__ int s_mm[2 * NW];
   __shared__ float s_lse[16 * KT];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1228,7 +1229,6 @@ void mx_paged_decode_balanced(
   const int TR = sh.tile_rows;                       // rows per partial slot
   const int UPS = sh.num_kv_heads * sh.row_tiles;    // units per sequence
   const int B = sh.batch;
-  const int alpha = sh.unit_overhead;
 
   // Empty sequences (L <= 0) are defined as zero output; sequence b's zeros (its seqlen_q *
   // num_heads consecutive rows) are written by workgroup b % num_groups.
@@ -1245,16 +1245,54 @@ void mx_paged_decode_balanced(
   // thread reads its few seq_lens once and keeps their weights in registers for both the total
   // and the scan that locates this workgroup's first position.
   constexpr int kScanPerThread = (512 + 64 * NW - 1) / (64 * NW);
-  auto weight = [&](int b, bool report) -> int {
-    const int seq = seq_extent<kAppend>(seq_lens, b, sh, status, report).sched;
-    return seq > 0 ? UPS * ((seq + kChunk - 1) / kChunk + alpha) : 0;
-  };
-  int wts[kScanPerThread];
-  int mine = 0;
+  int wts[kScanPerThread];  // chunks of the sequence, then its positions
+  int nb_lo = INT_MAX, nb_hi = 0;
 #pragma unroll
   for (int i = 0; i < kScanPerThread; ++i) {
     const int b = i * 64 * NW + tid;
-    wts[i] = b < B ? weight(b, wg == 0) : 0;
+    const int seq = b < B ? seq_extent<kAppend>(seq_lens, b, sh, status, wg == 0).sched : 0;
+    wts[i] = seq > 0 ? (seq + kChunk - 1) / kChunk : 0;
+    if (b < B) {
+      nb_lo = min(nb_lo, wts[i]);
+      nb_hi = max(nb_hi, wts[i]);
+    }
+  }
+  // Positions charged per unit on top of its chunks.  When every sequence has the same chunk
+  // count and the workgroups divide into k equal pieces per unit, the overhead is instead the
+  // smallest that makes k divide the unit's span: every workgroup then holds exactly one piece
+  // of equal chunks (charging the full overhead to a unit's first piece would leave its other
+  // pieces longer, and shares that straddle units would pay two pieces).
+  int alpha = sh.unit_overhead;
+  const int units = B * UPS;
+  if (sh.num_groups % units == 0) {  // the same in every thread: all reach the barrier
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      nb_lo = min(nb_lo, __shfl_xor(nb_lo, off));
+      nb_hi = max(nb_hi, __shfl_xor(nb_hi, off));
+    }
+    if (lane == 0) {
+      s_mm[wv] = nb_lo;
+      s_mm[NW + wv] = nb_hi;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2) {
+      nb_lo = min(nb_lo, s_mm[w2]);
+      nb_hi = max(nb_hi, s_mm[NW + w2]);
+    }
+    // Values read back from LDS are uniform, which the compiler cannot see: without the
+    // readfirstlane the unit walk below (and the page-id loads it feeds) would run per lane.
+    nb_lo = __builtin_amdgcn_readfirstlane(nb_lo);
+    nb_hi = __builtin_amdgcn_readfirstlane(nb_hi);
+    if (nb_lo == nb_hi && nb_lo > 0) {
+      const int k = sh.num_groups / units;
+      alpha = (k - nb_lo % k) % k;
+    }
+  }
+  int mine = 0;
+#pragma unroll
+  for (int i = 0; i < kScanPerThread; ++i) {
+    wts[i] = wts[i] > 0 ? UPS * (wts[i] + alpha) : 0;
     mine += wts[i];
   }
   // Total positions of the batch.

@@ -313,6 +313,35 @@ def test_balanced_empty_sequences(groups):
     _check(inp, out, batches=[1, 3, 5], label=f"empty groups={groups}")
 
 
+@pytest.mark.parametrize("sq,causal", [(1, False), (3, True)])
+@pytest.mark.parametrize("B,Hkv,L,groups", [
+    (1, 2, 100, 8),      # 7 chunks, 4 pieces per unit: overhead 1
+    (2, 4, 333, 16),     # 21 chunks, 2 pieces: overhead 1
+    (4, 2, 1000, 32),    # 63 chunks, 4 pieces: overhead 1
+    (3, 1, 257, 6),      # 17 chunks, 2 pieces: overhead 1
+    (8, 8, 64, 128),     # 4 chunks, 2 pieces: overhead 0
+    (2, 2, 17, 12),      # 2 chunks, 3 pieces: overhead 1, one piece per unit holds no chunk
+    (4, 4, 512, 48),     # 32 chunks, 3 pieces: overhead 1
+    (3, 2, 200, 10),     # workgroups not a multiple of the units: the usual overhead
+])
+def test_balanced_uniform_batch_equal_pieces(B, Hkv, L, groups, sq, causal):
+    """Every sequence of one length and the workgroups a multiple of the units: the balanced
+    schedule cuts each unit into equal pieces (the per-unit overhead becomes the smallest that
+    the piece count divides)."""
+    spec = W.custom_spec("uniform_bal", [L] * B, Hkv * 4, Hkv, 128, 16, seqlen_q=sq)
+    inp = W.make_inputs(spec, seed=B * L + groups, device=DEV)
+    label = f"uniform balanced B={B} Hkv={Hkv} L={L} groups={groups} sq={sq}"
+    print(label, flush=True)
+    out = paged_gqa_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_table, inp.seq_lens,
+                           inp.scale, causal=causal, num_splits=-groups)
+    torch.cuda.synchronize()
+    ref = paged_decode_reference(inp.q.cpu(), inp.k_cache.cpu(), inp.v_cache.cpu(),
+                                 inp.block_table.cpu(), inp.seq_lens.cpu(), inp.scale,
+                                 causal=causal)
+    assert_close_to_oracle(out.cpu(), ref, label)
+    assert read_device_status() == 0
+
+
 def test_balanced_matches_split_grid():
     inp = W.make_inputs("ragged", seed=14, device=DEV)
     a = _decode(inp, num_splits=0)
