@@ -39,6 +39,7 @@
 #include <cmath>
 #include <mutex>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "mx_paged_decode.h"
@@ -490,11 +491,16 @@ struct NoExtraChunk {
                                          const int (&)[KT], char*) const {}
 };
 
+// K/V cache pointers: restrict-qualified, except where the same launch also writes the cache
+// (the fused-append variants, through MainShape::k_dst / v_dst).
+template <bool kWrites>
+using CachePtr = std::conditional_t<kWrites, const uint16_t*, const uint16_t* __restrict__>;
+
 template <int D, int NBUF, int NW, bool kCausal, int KT, class Extra = NoExtraChunk>
 __device__ __forceinline__ void stream_chunks(SoftmaxState<D> (&st)[KT],
                                               const bf16x8 (&qop)[KT][D / 32],
-                                              const uint16_t* __restrict__ kc,
-                                              const uint16_t* __restrict__ vc,
+                                              CachePtr<!std::is_same_v<Extra, NoExtraChunk>> kc,
+                                              CachePtr<!std::is_same_v<Extra, NoExtraChunk>> vc,
                                               const int32_t* __restrict__ bt_row, int kv,
                                               int c_lo, int c_hi, int seq, int c_mask,
                                               const int (&row_lim)[KT], int wv, char* klds,
@@ -1025,8 +1031,8 @@ template <int D, int NBUF, int NW, bool kCausal, int KT, bool kAppend>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     KT == 2 ? 1 : (D == 64 ? MX_WAVES_PER_EU_D64 : (D == 128 ? MX_WAVES_PER_EU_D128 : MX_WAVES_PER_EU_D256)))))
 void mx_paged_decode_splitkv(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
-    const uint16_t* __restrict__ vc, uint16_t* __restrict__ out,
+    const uint16_t* __restrict__ q, CachePtr<kAppend> kc, CachePtr<kAppend> vc,
+    uint16_t* __restrict__ out,
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ block_table,
     float* __restrict__ part_o, float* __restrict__ part_lse, uint32_t* __restrict__ counters,
     uint32_t* __restrict__ status, const MainShape sh) {
@@ -1212,8 +1218,8 @@ template <int D, int NBUF, int NW, bool kCausal, int KT, bool kAppend>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     KT == 2 ? 1 : (D == 64 ? MX_WAVES_PER_EU_D64 : (D == 128 ? MX_WAVES_PER_EU_D128 : MX_WAVES_PER_EU_D256)))))
 void mx_paged_decode_balanced(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
-    const uint16_t* __restrict__ vc, uint16_t* __restrict__ out,
+    const uint16_t* __restrict__ q, CachePtr<kAppend> kc, CachePtr<kAppend> vc,
+    uint16_t* __restrict__ out,
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ block_table,
     float* __restrict__ part_o, float* __restrict__ part_lse, uint32_t* __restrict__ counters,
     uint32_t* __restrict__ status, const MainShape sh) {
