@@ -1270,7 +1270,8 @@ void mx_paged_decode_balanced(
   // pieces longer, and shares that straddle units would pay two pieces).
   int alpha = sh.unit_overhead;
   const int units = B * UPS;
-  if (sh.num_groups % units == 0) {  // the same in every thread: all reach the barrier
+  // (k = 1 needs no change: every workgroup then holds one whole unit whatever the charge.)
+  if (sh.num_groups > units && sh.num_groups % units == 0) {  // the same in every thread
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
       nb_lo = min(nb_lo, __shfl_xor(nb_lo, off));
