@@ -408,10 +408,11 @@ struct MainShape {
   // (written by the append kernel just before), so sequence b has max(seq_lens[b], 0) + appended
   // keys.  0 = seq_lens are the key counts.
   int appended;
-  // Append-and-attend in one launch (new_tokens = S in 1..16, else 0): the S new keys of each
-  // sequence are read from k_new / v_new [B, S, Hkv, D] as one extra masked chunk, attached to
-  // the schedule slot of the unit's last cache chunk (chunk 0 for an empty cache), and written to
-  // their cache slots at positions L + j (k_dst / v_dst) by the wave that loads them.
+  // Append-and-attend in one launch (new_tokens = S in 1..16, else 0; the kAppend kernel
+  // variants): the S new keys of each sequence are read from k_new / v_new [B, S, Hkv, D] as
+  // one extra masked chunk by the split or piece holding the unit's last schedule chunk (see
+  // NewTokens), and written to their cache slots at positions max(L, 0) + j through k_dst /
+  // v_dst, the same memory as the kernels' K/V cache pointers.
   const uint16_t* k_new;
   const uint16_t* v_new;
   uint16_t* k_dst;
