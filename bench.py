@@ -570,6 +570,10 @@ def main(argv=None) -> int:
                          "instead of the main workload and print its per-case lines and score")
     ap.add_argument("--graph", action="store_true",
                     help="also time the calls captured in a HIP graph and replayed")
+    ap.add_argument("--append-attend", action="store_true",
+                    help="time one decode step that appends a new token per sequence: the "
+                         "one-launch append-and-attend, the append kernel then the decode, "
+                         "and the decode alone (on --workload)")
     ap.add_argument("--shards", type=int, default=0,
                     help="also time the per-GPU pieces of the workload's decode sharded over N "
                          "GPUs' pages (partial decode per shard + merge), on this one GPU")
@@ -607,6 +611,11 @@ def main(argv=None) -> int:
             "reference_c500_sum_us": sum(C500_CLEAN_US.values()),
             "note": "score_c = round(100 R_c / (R_c + t_c)) with the reference's C500-fitted R_c"}),
             flush=True)
+        return 0
+
+    if args.append_attend:
+        print(json.dumps(time_append_attend(W.get_spec(args.workload), args.steps, args.warmup,
+                                            args.seed)), flush=True)
         return 0
 
     spec = W.get_spec(args.workload)
