@@ -156,7 +156,7 @@ def test_append_and_attend_shapes(D, P, Hkv, G, S, sq, ns):
     assert read_device_status() == 0
 
 
-@pytest.mark.parametrize("seed", range(40))
+@pytest.mark.parametrize("seed", range(80))
 def test_append_and_attend_random(seed):
     """Seeded random shapes, lengths (empty, negative, page boundaries), new-token counts
     1..16, query tokens, causal flag and schedule."""
@@ -167,7 +167,7 @@ def test_append_and_attend_random(seed):
     D = r.choice([64, 128, 256])
     P = r.choice([16, 32, 64, 128])
     Hkv = r.choice([1, 2, 4, 8])
-    G = r.choice([1, 2, 3, 4, 8, 16])
+    G = r.choice([1, 2, 3, 4, 7, 8, 16, 32])
     S = r.randint(1, 16)
     sq = r.choice([1, 1, 2, 4, S])
     B = r.randint(1, 6)
