@@ -474,11 +474,6 @@ __device__ __forceinline__ void load_q(bf16x8 (&qop)[D / 32], const uint16_t* q,
   }
 }
 
-// Streams chunks c_lo + wv + k*NW (k >= 0, < c_hi) of one (sequence, KV head) through this
-// wave's register ring, accumulating the KT row tiles into `st`.  The sequence holds `seq`
-// tokens; chunks from c_mask on (at least the last one) are processed with masks: tokens past
-// the sequence end, and with kCausal, for this lane's query row of tile t, the keys at or past
-// row_lim[t].  Without kCausal c_mask is the last chunk and row_lim is ignored.
 // A stream_chunks hook that does nothing (see NewTokens for the one that does).
 struct NoExtraChunk {
   template <int D>
@@ -497,6 +492,12 @@ struct NoExtraChunk {
 template <bool kWrites>
 using CachePtr = std::conditional_t<kWrites, const uint16_t*, const uint16_t* __restrict__>;
 
+// Streams chunks c_lo + wv + k*NW (k >= 0, < c_hi) of one (sequence, KV head) through this
+// wave's register ring, accumulating the KT row tiles into `st`.  The sequence holds `seq`
+// tokens; chunks from c_mask on (at least the last one) are processed with masks: tokens past
+// the sequence end, and with kCausal, for this lane's query row of tile t, the keys at or past
+// row_lim[t].  Without kCausal c_mask is the last chunk and row_lim is ignored.  `hook` may add
+// one more chunk from outside the cache (see NewTokens).
 template <int D, int NBUF, int NW, bool kCausal, int KT, class Extra = NoExtraChunk>
 __device__ __forceinline__ void stream_chunks(SoftmaxState<D> (&st)[KT],
                                               const bf16x8 (&qop)[KT][D / 32],
