@@ -28,6 +28,9 @@
 //    and merges cut units through a fan-in-8 tree of arrival counters.
 //  * Sharded decode: the same kernels can write each query row as fp32 output plus its
 //    log-sum-exp (mx_paged_gqa_decode_partial) for a cross-device merge (mx_lse_merge).
+//  * Paged K/V append (mx_paged_kv_append), and append-and-attend (mx_paged_gqa_decode_append):
+//    for up to 16 new tokens the kernels' kAppend variants read the new keys from k_new / v_new
+//    as one extra chunk per unit and write them to their cache slots in the same launch.
 
 #include <hip/hip_runtime.h>
 
@@ -56,9 +59,10 @@ typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
 constexpr int kChunk = 16;             // tokens per PV k-step (one 16x16x16 MFMA)
 constexpr float kRescaleSlack = 8.0f;  // log2 units the stale running max may lag behind
 // Workspace layout: [status word region][merge counters][partials].  The counter region has
-// a fixed size and offset and only the balanced kernel touches it (it resets every counter it
-// uses), so a zero-filled workspace keeps valid counters across calls of any shape, whatever
-// the partials of earlier calls left behind.
+// a fixed size and offset and holds the balanced kernel's merge-tree counters and the split
+// grid's per-unit arrival counters; every kernel resets each counter it uses, so a zero-filled
+// workspace keeps valid counters across calls of any shape, whatever the partials of earlier
+// calls left behind.
 constexpr int kStatusBytes = 256;
 constexpr int kMaxSlots = 4096 + 8192;          // balanced: workgroups + batch * Hkv
 constexpr int kCounterLevels = 4;               // fan-in-8 merge tree levels
@@ -1192,20 +1196,6 @@ void mx_paged_decode_splitkv(
 // ------------------------------------------------------------------------------------------
 
 constexpr int kMergeLevels = 4;  // enough for 8^4 = 4096 pieces per unit
-
-// Block-wide sum of one int per thread (all threads get the result).
-template <int NW>
-__device__ __forceinline__ int block_sum(int x, int* sred) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) sred[threadIdx.x >> 6] = x;
-  __syncthreads();
-  int t = 0;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) t += sred[w];
-  return t;
-}
 
 // One launch of num_groups workgroups covers the whole batch whatever the length mix.  Every
 // (sequence b, KV head and row group j) "unit" with n_b = ceil(L_b/16) > 0 chunks occupies n_b +
