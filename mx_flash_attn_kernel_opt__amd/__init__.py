@@ -9,6 +9,7 @@ exposes it over PyTorch-ROCm device tensors; it has no CPU fallback.
 from ._lib import MXAttnError, library_path, load  # noqa: F401
 from .decode import (  # noqa: F401
     BoundDecode,
+    BoundDecodeAppend,
     lse_merge,
     make_workspace,
     paged_gqa_decode,
@@ -24,6 +25,7 @@ from .shard import shard_pages  # noqa: F401
 
 __all__ = [
     "BoundDecode",
+    "BoundDecodeAppend",
     "MXAttnError",
     "library_path",
     "load",

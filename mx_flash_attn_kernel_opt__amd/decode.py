@@ -341,6 +341,19 @@ def paged_gqa_decode_append(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.T
     k_new / v_new as one more chunk and written to the cache by the same kernel); longer
     appends run the append kernel first.
     """
+    args, out = _append_call_args(q, k_new, v_new, k_cache, v_cache, block_table, seq_lens,
+                                  scale, out, causal, num_splits, max_seq_len, workspace)
+    dev = q.device
+    with torch.cuda.device(dev):
+        st = _lib.load().mx_paged_gqa_decode_append(*args, _stream_handle(stream, dev))
+    _lib.check(st)
+    return out
+
+
+def _append_call_args(q, k_new, v_new, k_cache, v_cache, block_table, seq_lens, scale, out,
+                      causal, num_splits, max_seq_len, workspace):
+    """Python-side checks of an append-and-attend call and its C arguments (all but the
+    stream), with the output tensor (allocated when ``out`` is None)."""
     dev, B, SQ, Hq, D, num_pages, P, Hkv = _check_decode_inputs(q, k_cache, v_cache,
                                                                 block_table, seq_lens)
     _require(k_new.shape == v_new.shape, "k_new and v_new must have the same shape")
@@ -362,14 +375,39 @@ def paged_gqa_decode_append(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.T
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     ws_bytes = _workspace_bytes(workspace, dev)
-    with torch.cuda.device(dev):
-        st = _lib.load().mx_paged_gqa_decode_append(
-            _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache), _ptr(out),
+    args = [_ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache), _ptr(out),
             _ptr(seq_lens), _ptr(block_table), B, SQ, S, Hq, Hkv, D, P, num_pages,
             block_table.shape[1], max_seq_len, int(bool(causal)), float(scale), num_splits,
-            _ptr(workspace), ws_bytes, _stream_handle(stream, dev))
-    _lib.check(st)
-    return out
+            _ptr(workspace), ws_bytes]
+    return args, out
+
+
+class BoundDecodeAppend:
+    """An append-and-attend call (``paged_gqa_decode_append``) with its C arguments prepared
+    once, for serving loops: each ``__call__()`` appends the current contents of k_new / v_new
+    at the current seq_lens and attends, with no Python-side work beyond the C call.
+
+    The constructor checks the tensors and launches nothing (an append has side effects); the
+    library validates the arguments again on every call and raises on a bad status.  The bound
+    tensors must stay alive and keep their storage; update seq_lens (and q, k_new, v_new) in
+    place between calls.
+    """
+
+    def __init__(self, q, k_new, v_new, k_cache, v_cache, block_table, seq_lens, scale=None, *,
+                 out=None, causal: bool = False, num_splits: int = 0, max_seq_len: int = 0,
+                 workspace=None, stream=None):
+        self._args, self.out = _append_call_args(q, k_new, v_new, k_cache, v_cache,
+                                                 block_table, seq_lens, scale, out, causal,
+                                                 num_splits, max_seq_len, workspace)
+        self._keep = (q, k_new, v_new, k_cache, v_cache, block_table, seq_lens, workspace)
+        self._fn = _lib.load().mx_paged_gqa_decode_append
+        self._stream = _stream_handle(stream, q.device)
+
+    def __call__(self) -> torch.Tensor:
+        st = self._fn(*self._args, self._stream)
+        if st != _lib.MX_STATUS_OK:
+            _lib.check(st)
+        return self.out
 
 
 def read_device_status(workspace: torch.Tensor | None = None, reset: bool = True,

@@ -248,3 +248,33 @@ def test_append_and_attend_of_zero_tokens_is_the_decode():
     plain = paged_gqa_decode(qd, kd, vd, td, ld)
     torch.cuda.synchronize()
     assert torch.equal(fused, plain) and torch.equal(kd.cpu(), k) and torch.equal(vd.cpu(), v)
+
+
+def test_bound_append_and_attend_serving_loop():
+    """Three decode steps through BoundDecodeAppend, with seq_lens advanced and the new rows
+    written in place between calls, equal three paged_gqa_decode_append calls on a copy of the
+    cache bit for bit (same entry point, same plan), and the pools end identical."""
+    from mx_flash_attn_kernel_opt__amd import BoundDecodeAppend, paged_gqa_decode_append
+    lens = [5, 100, 1000, 0]
+    k, v, table, kn, vn, q, lens_t = _fused_case(lens, 4, 1, seed=33)
+    B, Hkv, D = len(lens), 8, 128
+    g = torch.Generator().manual_seed(34)
+    steps = [(torch.randn(B, 1, Hkv, D, generator=g).to(torch.bfloat16),
+              torch.randn(B, 1, Hkv, D, generator=g).to(torch.bfloat16)) for _ in range(3)]
+    kd1, vd1, kd2, vd2 = k.to(DEV), v.to(DEV), k.to(DEV), v.to(DEV)
+    td, qd = table.to(DEV), q[:, 0].to(DEV)
+    ld1, ld2 = lens_t.to(DEV), lens_t.to(DEV)
+    kn_d = torch.empty(B, 1, Hkv, D, dtype=torch.bfloat16, device=DEV)
+    vn_d = torch.empty_like(kn_d)
+    bound = BoundDecodeAppend(qd, kn_d, vn_d, kd1, vd1, td, ld1)
+    for kn_s, vn_s in steps:
+        kn_d.copy_(kn_s)
+        vn_d.copy_(vn_s)
+        a = bound().clone()
+        b = paged_gqa_decode_append(qd, kn_d, vn_d, kd2, vd2, td, ld2)
+        ld1 += 1
+        ld2 += 1
+        torch.cuda.synchronize()
+        assert torch.equal(a, b)
+    assert torch.equal(kd1, kd2) and torch.equal(vd1, vd2)
+    assert read_device_status() == 0
