@@ -128,6 +128,26 @@ int mx_paged_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
                         int32_t phase, void* stream);
 
 /*
+ * The decode over an fp8 K/V cache: k_cache and v_cache hold OCP e4m3fn bytes (torch
+ * float8_e4m3fn) in the same [num_pages, page_size, num_kv_heads, head_dim] layout, and the
+ * keys and values are k_scale and v_scale times the stored values (per-tensor scales, as in
+ * vLLM's fp8 KV cache).  q and out stay bf16; every other argument is as mx_paged_gqa_decode's.
+ * The kernels read half the bytes of a bf16 cache and widen the values to bf16 in registers
+ * (exact: every e4m3fn value is a bf16 value) before the same MFMA path.  k_scale and v_scale
+ * must be finite.
+ * No counterpart in the reference, whose cache is bf16 only; it is the same operator on a
+ * narrower cache format.
+ */
+int mx_paged_gqa_decode_fp8kv(const void* q, const void* k_cache, const void* v_cache,
+                              void* out, const int32_t* seq_lens, const int32_t* block_table,
+                              int64_t batch, int64_t seqlen_q, int64_t num_heads,
+                              int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                              int64_t num_pages, int64_t max_pages_per_seq, int64_t max_seq_len,
+                              int32_t causal, float scale, float k_scale, float v_scale,
+                              int64_t num_splits, void* workspace, int64_t workspace_bytes,
+                              int32_t phase, void* stream);
+
+/*
  * Partial decode of one shard of the keys (the split phase of the reference's split-KV decode,
  * optimized_c500_flash_attn.cu:537-551 and the partial (m, l, O) rows it leaves for
  * combine_splits, exposed for a caller-chosen key range).  Arguments as mx_paged_gqa_decode,

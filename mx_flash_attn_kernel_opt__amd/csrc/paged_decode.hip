@@ -279,6 +279,108 @@ __device__ __forceinline__ void k_operands(bf16x8 (&kop)[D / 32], const Chunk<D>
   }
 }
 
+// ------------------------------------------------------------------------------------------
+// fp8 K/V cache (OCP e4m3fn, one byte per element, per-tensor scales)
+// ------------------------------------------------------------------------------------------
+
+// Register image of one 16-token chunk of one KV head of an fp8 cache (half the bytes of a
+// bf16 chunk, loaded in the same row-major patterns):
+//   k[i]    : 16 fp8 values, K[token i*(1024/D) + lane/(D/16)][16*(lane%(D/16)) .. +15]
+//   v[r][w] : V[token 4*g4 + r][(D/16)*r16 + 4w .. +3]   (D/64 dwords per row)
+template <int D>
+struct Chunk8 {
+  u32x4 k[D / 64];
+  uint32_t v[4][D / 64];
+};
+
+// Two fp8 (e4m3fn) values of dword x (bytes 0-1, or 2-3 with kHi) as one dword of two bf16:
+// exact, since every e4m3fn value is a bf16 value.  One gfx950 v_cvt_scalef32_pk_bf16_fp8 with
+// scale 1, which reads the OCP e4m3fn format (checked against torch's float8_e4m3fn on all 256
+// codes, NaN included).
+template <bool kHi>
+__device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t x) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x, 1.0f, kHi));
+}
+
+template <int D>
+__device__ __forceinline__ void k_lane_offsets8(LaneOffsets& lo, int lane, int kv) {
+  constexpr int SPR = D / 16;    // 16-byte segments per fp8 K row
+  constexpr int RPI = 64 / SPR;  // rows per load instruction
+  lo.k = (uint32_t)(lane / SPR) * lo.token_bytes + (uint32_t)(kv * D) + 16u * (lane % SPR);
+  lo.k_step = RPI * lo.token_bytes;
+}
+
+template <int D>
+__device__ __forceinline__ void load_chunk(Chunk8<D>& c, const uint8_t* kpage,
+                                           const uint8_t* vpage, const LaneOffsets& lo) {
+  const uint16_t* kp = reinterpret_cast<const uint16_t*>(kpage);
+  const uint16_t* vp = reinterpret_cast<const uint16_t*>(vpage);
+#pragma unroll
+  for (int i = 0; i < D / 64; ++i)
+    c.k[i] = ld_kv16<MX_K_NONTEMPORAL != 0>(kp, lo.k + (uint32_t)i * lo.k_step);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint32_t off = lo.v + r * lo.token_bytes;
+    if constexpr (D == 64) {
+      const uint32_t* p = reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(vp) + off);
+      c.v[r][0] = MX_V_NONTEMPORAL ? __builtin_nontemporal_load(p) : *p;
+    } else if constexpr (D == 128) {
+      const u32x2 x = ld_kv8<MX_V_NONTEMPORAL != 0>(vp, off);
+      c.v[r][0] = x[0];
+      c.v[r][1] = x[1];
+    } else {
+      const u32x4 x = ld_kv16<MX_V_NONTEMPORAL != 0>(vp, off);
+      c.v[r][0] = x[0];
+      c.v[r][1] = x[1];
+      c.v[r][2] = x[2];
+      c.v[r][3] = x[3];
+    }
+  }
+}
+
+// K staging of an fp8 chunk: each lane widens its 16 values to bf16 and writes them as two
+// 16-byte segments of the same swizzled LDS tile as a bf16 chunk, so the operand read back is
+// unchanged.
+template <int D>
+__device__ __forceinline__ void k_operands(bf16x8 (&kop)[D / 32], const Chunk8<D>& c,
+                                           char* klds, int lane) {
+  static_assert(k_via_lds<D>(), "fp8 K chunks are staged through LDS");
+  constexpr int SPR = D / 16;
+  constexpr int RPI = 64 / SPR;
+  const int wr = lane / SPR;
+  const int ws = lane % SPR;
+#pragma unroll
+  for (int i = 0; i < D / 64; ++i) {
+    const int row = i * RPI + wr;
+    const u32x4 x = c.k[i];
+    const u32x4 lo = {fp8x2_to_bf16x2<false>(x[0]), fp8x2_to_bf16x2<true>(x[0]),
+                      fp8x2_to_bf16x2<false>(x[1]), fp8x2_to_bf16x2<true>(x[1])};
+    const u32x4 hi = {fp8x2_to_bf16x2<false>(x[2]), fp8x2_to_bf16x2<true>(x[2]),
+                      fp8x2_to_bf16x2<false>(x[3]), fp8x2_to_bf16x2<true>(x[3])};
+    char* base = klds + row * 2 * D;
+    *reinterpret_cast<u32x4*>(base + 16 * ((2 * ws) ^ k_swizzle<D>(row))) = lo;
+    *reinterpret_cast<u32x4*>(base + 16 * ((2 * ws + 1) ^ k_swizzle<D>(row))) = hi;
+  }
+  const int t = lane & 15;
+  const int g4 = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i)
+    kop[i] = __builtin_bit_cast(
+        bf16x8, *reinterpret_cast<const u32x4*>(klds + t * 2 * D +
+                                                16 * ((4 * i + g4) ^ k_swizzle<D>(t))));
+}
+
+// Dword w (elements 2w, 2w+1 of this lane's slice) of V row r of a chunk, as bf16.
+template <int D>
+__device__ __forceinline__ uint32_t v_word(const Chunk<D>& c, int r, int w) {
+  return c.v[r][w];
+}
+template <int D>
+__device__ __forceinline__ uint32_t v_word(const Chunk8<D>& c, int r, int w) {
+  const uint32_t x = c.v[r][w >> 1];
+  return (w & 1) ? fp8x2_to_bf16x2<true>(x) : fp8x2_to_bf16x2<false>(x);
+}
+
 // Initial running max: finite, so exp2(score - m) is 0 for a masked (-inf) score even before a
 // row has seen any visible key; a row that never sees one keeps l == 0 and is written as zeros.
 constexpr float kNoScore = -1.0e30f;
@@ -304,8 +406,8 @@ __device__ __forceinline__ void reset_state(SoftmaxState<D>& st) {
 // reach the accumulators), and this lane's query row of tile t sees only the first
 // row_valid[t] (<= nvalid) tokens: the causal limit of multi-token queries.  Scores of tokens
 // a row does not see become -inf.
-template <int D, bool kMasked, int KT>
-__device__ __forceinline__ void process_chunk(SoftmaxState<D> (&st)[KT], const Chunk<D>& c,
+template <int D, bool kMasked, int KT, class ChunkT>
+__device__ __forceinline__ void process_chunk(SoftmaxState<D> (&st)[KT], const ChunkT& c,
                                               const bf16x8 (&qop)[KT][D / 32], float scale_log2,
                                               int g4, int nvalid, const int (&row_valid)[KT],
                                               char* klds, int lane) {
@@ -354,7 +456,7 @@ __device__ __forceinline__ void process_chunk(SoftmaxState<D> (&st)[KT], const C
   for (int r = 0; r < 4; ++r) {
     const bool keep = !kMasked || (4 * g4 + r < nvalid);
 #pragma unroll
-    for (int w = 0; w < D / 32; ++w) v[r][w] = keep ? c.v[r][w] : 0u;
+    for (int w = 0; w < D / 32; ++w) v[r][w] = keep ? v_word<D>(c, r, w) : 0u;
   }
   // O^T[d][row] += V^T . P^T  (tile i covers dims (D/16)*m + i, m = 0..15)
 #pragma unroll
@@ -422,7 +524,21 @@ struct MainShape {
   uint16_t* k_dst;
   uint16_t* v_dst;
   int new_tokens;
+  // fp8 caches: V values are v_scale times the stored fp8 values (the K scale is folded into
+  // scale_log2 on the host).
+  float v_scale;
 };
+
+// fp8 caches: a wave's output accumulators were built from unscaled V; O is linear in V, so
+// scaling them once before the merge applies v_scale exactly as the per-element product would.
+template <int D, int KT>
+__device__ __forceinline__ void scale_o_by_v_scale(SoftmaxState<D> (&st)[KT],
+                                                   const MainShape& sh) {
+#pragma unroll
+  for (int t = 0; t < KT; ++t)
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) st[t].o[i] *= sh.v_scale;
+}
 
 // Keys of sequence b before clamping (see MainShape::appended).
 __device__ __forceinline__ int key_count(const int32_t* seq_lens, int b, int appended) {
@@ -480,10 +596,10 @@ __device__ __forceinline__ void load_q(bf16x8 (&qop)[D / 32], const uint16_t* q,
 
 // A stream_chunks hook that does nothing (see NewTokens for the one that does).
 struct NoExtraChunk {
-  template <int D>
-  __device__ __forceinline__ void load(Chunk<D>&) const {}
-  template <int D, int KT>
-  __device__ __forceinline__ void process(SoftmaxState<D> (&)[KT], const Chunk<D>&,
+  template <class ChunkT>
+  __device__ __forceinline__ void load(ChunkT&) const {}
+  template <int D, int KT, class ChunkT>
+  __device__ __forceinline__ void process(SoftmaxState<D> (&)[KT], const ChunkT&,
                                           const bf16x8 (&)[KT][D / 32], const int (&)[KT],
                                           char*) const {}
   template <int D, int KT>
@@ -493,8 +609,15 @@ struct NoExtraChunk {
 
 // K/V cache pointers: restrict-qualified, except where the same launch also writes the cache
 // (the fused-append variants, through MainShape::k_dst / v_dst).
-template <bool kWrites>
-using CachePtr = std::conditional_t<kWrites, const uint16_t*, const uint16_t* __restrict__>;
+// Elements are uint16_t (bf16) or uint8_t (fp8).
+template <bool kWrites, class Elem = uint16_t>
+using CachePtr = std::conditional_t<kWrites, const Elem*, const Elem* __restrict__>;
+
+// Cache element and chunk register image of a bf16 (kFp8 false) or fp8 cache.
+template <bool kFp8>
+using CacheElem = std::conditional_t<kFp8, uint8_t, uint16_t>;
+template <int D, bool kFp8>
+using ChunkOf = std::conditional_t<kFp8, Chunk8<D>, Chunk<D>>;
 
 // Streams chunks c_lo + wv + k*NW (k >= 0, < c_hi) of one (sequence, KV head) through this
 // wave's register ring, accumulating the KT row tiles into `st`.  The sequence holds `seq`
@@ -502,11 +625,14 @@ using CachePtr = std::conditional_t<kWrites, const uint16_t*, const uint16_t* __
 // the sequence end, and with kCausal, for this lane's query row of tile t, the keys at or past
 // row_lim[t].  Without kCausal c_mask is the last chunk and row_lim is ignored.  `hook` may add
 // one more chunk from outside the cache (see NewTokens).
-template <int D, int NBUF, int NW, bool kCausal, int KT, class Extra = NoExtraChunk>
+template <int D, int NBUF, int NW, bool kCausal, int KT, class Extra = NoExtraChunk,
+          bool kFp8 = false>
 __device__ __forceinline__ void stream_chunks(SoftmaxState<D> (&st)[KT],
                                               const bf16x8 (&qop)[KT][D / 32],
-                                              CachePtr<!std::is_same_v<Extra, NoExtraChunk>> kc,
-                                              CachePtr<!std::is_same_v<Extra, NoExtraChunk>> vc,
+                                              CachePtr<!std::is_same_v<Extra, NoExtraChunk>,
+                                                       CacheElem<kFp8>> kc,
+                                              CachePtr<!std::is_same_v<Extra, NoExtraChunk>,
+                                                       CacheElem<kFp8>> vc,
                                               const int32_t* __restrict__ bt_row, int kv,
                                               int c_lo, int c_hi, int seq, int c_mask,
                                               const int (&row_lim)[KT], int wv, char* klds,
@@ -516,10 +642,15 @@ __device__ __forceinline__ void stream_chunks(SoftmaxState<D> (&st)[KT],
   const int lane = threadIdx.x & 63;
   const int r16 = lane & 15;
   const int g4 = lane >> 4;
+  constexpr uint32_t kElemBytes = sizeof(CacheElem<kFp8>);
   LaneOffsets lo;
-  lo.token_bytes = 2u * (uint32_t)sh.token_stride;
-  k_lane_offsets<D>(lo, lane, kv);
-  lo.v = 2u * (uint32_t)(4 * g4 * sh.token_stride + kv * D + VW * r16);
+  lo.token_bytes = kElemBytes * (uint32_t)sh.token_stride;
+  if constexpr (kFp8) {
+    k_lane_offsets8<D>(lo, lane, kv);
+  } else {
+    k_lane_offsets<D>(lo, lane, kv);
+  }
+  lo.v = kElemBytes * (uint32_t)(4 * g4 * sh.token_stride + kv * D + VW * r16);
   const int chunk_mask = (1 << sh.chunk_shift) - 1;
   const float sl2 = sh.scale_log2;
 
@@ -537,7 +668,8 @@ __device__ __forceinline__ void stream_chunks(SoftmaxState<D> (&st)[KT],
   auto gc = [&](int k) { return c_lo + wv + k * NW; };
   // Masked processing of this wave's k-th chunk: tokens of the chunk inside the sequence, and
   // those this lane's row sees.
-  auto masked = [&](Chunk<D>& cb, int k) {
+  using ChunkT = ChunkOf<D, kFp8>;
+  auto masked = [&](ChunkT& cb, int k) {
     const int t0 = gc(k) * kChunk;
     const int nvalid = min(kChunk, seq - t0);
     int row_valid[KT];
@@ -549,12 +681,12 @@ __device__ __forceinline__ void stream_chunks(SoftmaxState<D> (&st)[KT],
 #pragma unroll
   for (int t = 0; t < KT; ++t) all_valid[t] = kChunk;
 
-  Chunk<D> buf[NBUF];
-  auto load = [&](Chunk<D>& dst, int64_t base) { load_chunk<D>(dst, kc + base, vc + base, lo); };
+  ChunkT buf[NBUF];
+  auto load = [&](ChunkT& dst, int64_t base) { load_chunk<D>(dst, kc + base, vc + base, lo); };
   // The hook's extra chunk is loaded before the ring's first chunks and processed once they
   // are in flight, so its memory latency overlaps theirs (or, where registers are short, all
   // of it runs in hook.finish after the ring).
-  Chunk<D> xc;
+  ChunkT xc;
   hook.load(xc);
 
   // Register ring of NBUF chunks.  The steady-state loops process NBUF chunks and refill their
@@ -1033,15 +1165,17 @@ __device__ __forceinline__ void acquire_partials() {
 // split and row.  With fused_combine the last split of each unit to finish (a device-scope
 // arrival counter per unit) merges them itself, so the whole call is one launch; otherwise
 // mx_paged_decode_combine merges them in a second launch.
-template <int D, int NBUF, int NW, bool kCausal, int KT, bool kAppend>
+template <int D, int NBUF, int NW, bool kCausal, int KT, bool kAppend, bool kFp8>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     KT == 2 ? 1 : (D == 64 ? MX_WAVES_PER_EU_D64 : (D == 128 ? MX_WAVES_PER_EU_D128 : MX_WAVES_PER_EU_D256)))))
 void mx_paged_decode_splitkv(
-    const uint16_t* __restrict__ q, CachePtr<kAppend> kc, CachePtr<kAppend> vc,
+    const uint16_t* __restrict__ q, CachePtr<kAppend, CacheElem<kFp8>> kc,
+    CachePtr<kAppend, CacheElem<kFp8>> vc,
     uint16_t* __restrict__ out,
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ block_table,
     float* __restrict__ part_o, float* __restrict__ part_lse, uint32_t* __restrict__ counters,
     uint32_t* __restrict__ status, const MainShape sh) {
+  static_assert(!(kAppend && kFp8), "the fused append writes bf16 caches only");
   using L = GroupLds<D, NW, KT>;
   __shared__ __attribute__((aligned(16))) char lds[L::kBytes];
   __shared__ int s_last;
@@ -1105,9 +1239,11 @@ void mx_paged_decode_splitkv(
                                             c_mask, row_lim, wv, L::ktile(lds, wv), sh, bad_page,
                                             nt);
   } else {
-    stream_chunks<D, NBUF, NW, kCausal, KT>(st, qop, kc, vc, bt_row, kv, c_lo, c_end, ext.cache,
-                                            c_mask, row_lim, wv, L::ktile(lds, wv), sh, bad_page);
+    stream_chunks<D, NBUF, NW, kCausal, KT, NoExtraChunk, kFp8>(
+        st, qop, kc, vc, bt_row, kv, c_lo, c_end, ext.cache, c_mask, row_lim, wv,
+        L::ktile(lds, wv), sh, bad_page);
   }
+  if constexpr (kFp8) scale_o_by_v_scale<D, KT>(st, sh);
   if (bad_page && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
   publish_wave_state<D, NW, KT>(lds, st, wv);
   for (int e = tid; e < nrows * (D / 4); e += 64 * NW) {
@@ -1206,15 +1342,17 @@ constexpr int kMergeLevels = 4;  // enough for 8^4 = 4096 pieces per unit
 // entirely is written out as bf16; a unit cut into several pieces has each piece written as
 // a normalised partial (O/l, log2-sum-exp) to its own slot, and the last piece to finish
 // merges them through a fan-in-8 tree of per-unit counters, so the whole call is one launch.
-template <int D, int NBUF, int NW, bool kCausal, int KT, bool kAppend>
+template <int D, int NBUF, int NW, bool kCausal, int KT, bool kAppend, bool kFp8>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     KT == 2 ? 1 : (D == 64 ? MX_WAVES_PER_EU_D64 : (D == 128 ? MX_WAVES_PER_EU_D128 : MX_WAVES_PER_EU_D256)))))
 void mx_paged_decode_balanced(
-    const uint16_t* __restrict__ q, CachePtr<kAppend> kc, CachePtr<kAppend> vc,
+    const uint16_t* __restrict__ q, CachePtr<kAppend, CacheElem<kFp8>> kc,
+    CachePtr<kAppend, CacheElem<kFp8>> vc,
     uint16_t* __restrict__ out,
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ block_table,
     float* __restrict__ part_o, float* __restrict__ part_lse, uint32_t* __restrict__ counters,
     uint32_t* __restrict__ status, const MainShape sh) {
+  static_assert(!(kAppend && kFp8), "the fused append writes bf16 caches only");
   using L = GroupLds<D, NW, KT>;
   __shared__ __attribute__((aligned(16))) char lds[L::kBytes];
   __shared__ int s_int[NW + 4];
@@ -1389,10 +1527,11 @@ void mx_paged_decode_balanced(
                                                 ext.cache, c_mask, row_lim, wv,
                                                 L::ktile(lds, wv), sh, bad_page, nt);
       } else {
-        stream_chunks<D, NBUF, NW, kCausal, KT>(st, qop, kc, vc, bt_row, kv, ca, c_end,
-                                                ext.cache, c_mask, row_lim, wv,
-                                                L::ktile(lds, wv), sh, bad_page);
+        stream_chunks<D, NBUF, NW, kCausal, KT, NoExtraChunk, kFp8>(
+            st, qop, kc, vc, bt_row, kv, ca, c_end, ext.cache, c_mask, row_lim, wv,
+            L::ktile(lds, wv), sh, bad_page);
       }
+      if constexpr (kFp8) scale_o_by_v_scale<D, KT>(st, sh);
       publish_wave_state<D, NW, KT>(lds, st, wv);
 
       if (npieces == 1) {
@@ -1965,14 +2104,41 @@ struct AppendArgs {
   const void* v_new = nullptr;
 };
 
+// Format of the K/V cache: bf16, or fp8 (OCP e4m3fn) whose K and V values are k_scale and
+// v_scale times the stored ones.
+struct KvFormat {
+  bool fp8 = false;
+  float k_scale = 1.0f;
+  float v_scale = 1.0f;
+};
+
+// Register ring depth of the fp8 kernels (an fp8 chunk takes half the registers of a bf16 one).
+// (A/B on 512 MB fp8 caches, chunks per ring 2/3/4/6: D=64 173.6/174.7/183.0/186.2 us, D=128
+// config-2 shape 95.8/93.2/95.7/96.4 us, D=256 1/2/3 chunks 93.3/95.0/104.1 us.)
+#ifndef MX_NBUF8_D64
+#define MX_NBUF8_D64 2
+#endif
+#ifndef MX_NBUF8_D128
+#define MX_NBUF8_D128 3
+#endif
+#ifndef MX_NBUF8_D256
+#define MX_NBUF8_D256 1
+#endif
+template <int D>
+constexpr int ring_depth_fp8() {
+  return D == 64 ? MX_NBUF8_D64 : (D == 128 ? MX_NBUF8_D128 : MX_NBUF8_D256);
+}
+
 template <int D, bool kCausal, int KT>
 hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v, void* out,
                   const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
                   int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads, int64_t page_size,
                   int64_t num_pages, int64_t max_pages, float scale, char* ws, int32_t phase,
-                  float* o_out, float* lse_out, const AppendArgs& app, hipStream_t stream) {
+                  float* o_out, float* lse_out, const AppendArgs& app, const KvFormat& kv,
+                  hipStream_t stream) {
   constexpr int kNW = waves_per_group<D>();
   constexpr int kNBUF = ring_depth<D>();
+  constexpr int kNBUF8 = ring_depth_fp8<D>();
   MainShape sh;
   sh.page_stride = page_size * num_kv_heads * D;
   sh.token_stride = (int)(num_kv_heads * D);
@@ -1990,7 +2156,8 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   sh.num_pages = (num_pages > 0 && num_pages <= INT32_MAX) ? (int)num_pages : 0;
   sh.chunk_shift = plan.chunk_shift;
   sh.cap_tokens = (int)plan.cap_tokens;
-  sh.scale_log2 = scale * 1.4426950408889634f;
+  sh.scale_log2 = scale * 1.4426950408889634f * (kv.fp8 ? kv.k_scale : 1.0f);
+  sh.v_scale = kv.fp8 ? kv.v_scale : 1.0f;
   sh.num_splits = (int)plan.splits;
   sh.fused_combine = 0;
   sh.tokens_per_split = (int)plan.tokens_per_split;
@@ -2010,20 +2177,29 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   // The fused-append variants of the main kernels load the new keys in the LDS-staged K layout.
   constexpr bool kCanAppend = k_via_lds<D>();
   const bool append = app.new_tokens > 0;
-  if (append && !kCanAppend) return hipErrorInvalidValue;
+  if (append && (!kCanAppend || kv.fp8)) return hipErrorInvalidValue;
+  const uint16_t* q16 = static_cast<const uint16_t*>(q);
+  const uint16_t* k16 = static_cast<const uint16_t*>(k);
+  const uint16_t* v16 = static_cast<const uint16_t*>(v);
+  const uint8_t* k8 = static_cast<const uint8_t*>(k);
+  const uint8_t* v8 = static_cast<const uint8_t*>(v);
 
   if (plan.schedule == MX_SCHEDULE_BALANCED) {
     // One launch does everything; MX_PHASE_COMBINE_ONLY has nothing left to do.
     if (phase == MX_PHASE_COMBINE_ONLY) return hipSuccess;
-    const auto kernel = append ? mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, kCanAppend>
-                               : mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, false>;
-    hipLaunchKernelGGL(kernel, dim3((unsigned)plan.groups),
-                       dim3(64 * kNW), 0, stream, static_cast<const uint16_t*>(q),
-                       static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
-                       static_cast<uint16_t*>(out), seq_lens, block_table,
-                       reinterpret_cast<float*>(ws + plan.o_offset),
-                       reinterpret_cast<float*>(ws + plan.lse_offset),
-                       reinterpret_cast<uint32_t*>(ws + plan.counter_offset), status, sh);
+    auto go = [&](auto kernel, auto kc, auto vc) {
+      hipLaunchKernelGGL(kernel, dim3((unsigned)plan.groups), dim3(64 * kNW), 0, stream, q16, kc,
+                         vc, static_cast<uint16_t*>(out), seq_lens, block_table,
+                         reinterpret_cast<float*>(ws + plan.o_offset),
+                         reinterpret_cast<float*>(ws + plan.lse_offset),
+                         reinterpret_cast<uint32_t*>(ws + plan.counter_offset), status, sh);
+    };
+    if (kv.fp8)
+      go(mx_paged_decode_balanced<D, kNBUF8, kNW, kCausal, KT, false, true>, k8, v8);
+    else if (append)
+      go(mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, kCanAppend, false>, k16, v16);
+    else
+      go(mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, false, false>, k16, v16);
     return hipGetLastError();
   }
 
@@ -2040,13 +2216,17 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   if (phase != MX_PHASE_COMBINE_ONLY) {
     const dim3 grid((unsigned)(num_kv_heads * plan.row_tiles), (unsigned)batch,
                     (unsigned)plan.splits);
-    const auto kernel = append ? mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT, kCanAppend>
-                               : mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT, false>;
-    hipLaunchKernelGGL(kernel, grid, dim3(64 * kNW), 0, stream, static_cast<const uint16_t*>(q),
-                       static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
-                       static_cast<uint16_t*>(out), seq_lens,
-                       block_table, part_o, part_lse,
-                       reinterpret_cast<uint32_t*>(ws + kStatusBytes), status, sh);
+    auto go = [&](auto kernel, auto kc, auto vc) {
+      hipLaunchKernelGGL(kernel, grid, dim3(64 * kNW), 0, stream, q16, kc, vc,
+                         static_cast<uint16_t*>(out), seq_lens, block_table, part_o, part_lse,
+                         reinterpret_cast<uint32_t*>(ws + kStatusBytes), status, sh);
+    };
+    if (kv.fp8)
+      go(mx_paged_decode_splitkv<D, kNBUF8, kNW, kCausal, KT, false, true>, k8, v8);
+    else if (append)
+      go(mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT, kCanAppend, false>, k16, v16);
+    else
+      go(mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT, false, false>, k16, v16);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -2145,7 +2325,8 @@ int run_decode(const Plan& plan, const void* q, const void* k_cache, const void*
                const int32_t* block_table, int64_t batch, int64_t seqlen_q, int64_t num_heads,
                int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_pages,
                int64_t max_pages_per_seq, int32_t causal, float scale, void* workspace,
-               int32_t phase, const AppendArgs& app, void* stream) {
+               int32_t phase, const AppendArgs& app, void* stream,
+               const KvFormat& kv = KvFormat{}) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   hipError_t e;
@@ -2154,7 +2335,7 @@ int run_decode(const Plan& plan, const void* q, const void* k_cache, const void*
 #define MX_LAUNCH(DIM, CAUSAL, KT)                                                            \
   launch<DIM, CAUSAL, KT>(plan, q, k_cache, v_cache, out, seq_lens, block_table, batch, seqlen_q, \
                       num_heads, num_kv_heads, page_size, num_pages, max_pages_per_seq, scale, \
-                      ws, phase, o_out, lse_out, app, s)
+                      ws, phase, o_out, lse_out, app, kv, s)
   const bool pair = plan.tiles_per_group == 2;
   switch (head_dim) {
     case 64:
@@ -2182,7 +2363,8 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* o
                 int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads,
                 int64_t head_dim, int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
                 int64_t max_seq_len, int32_t causal, float scale, int64_t num_splits,
-                void* workspace, int64_t workspace_bytes, int32_t phase, void* stream) {
+                void* workspace, int64_t workspace_bytes, int32_t phase, void* stream,
+                const KvFormat& kv = KvFormat{}) {
   Plan plan;
   const int st = prepare_decode(q, k_cache, v_cache, out, batch, seqlen_q, num_heads,
                                 num_kv_heads, head_dim, page_size, num_pages, max_pages_per_seq,
@@ -2191,7 +2373,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* o
   if (st != MX_STATUS_OK) return st;
   return run_decode(plan, q, k_cache, v_cache, out, o_out, lse_out, seq_lens, block_table, batch,
                     seqlen_q, num_heads, num_kv_heads, head_dim, page_size, num_pages,
-                    max_pages_per_seq, causal, scale, workspace, phase, AppendArgs{}, stream);
+                    max_pages_per_seq, causal, scale, workspace, phase, AppendArgs{}, stream, kv);
 }
 
 // Argument checks of a paged K/V append (shared by mx_paged_kv_append and the fused
@@ -2260,6 +2442,31 @@ int mx_paged_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
                      seqlen_q, num_heads, num_kv_heads, head_dim, page_size, num_pages,
                      max_pages_per_seq, max_seq_len, causal, scale, num_splits, workspace,
                      workspace_bytes, phase, stream);
+}
+
+int mx_paged_gqa_decode_fp8kv(const void* q, const void* k_cache, const void* v_cache,
+                              void* out, const int32_t* seq_lens, const int32_t* block_table,
+                              int64_t batch, int64_t seqlen_q, int64_t num_heads,
+                              int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                              int64_t num_pages, int64_t max_pages_per_seq, int64_t max_seq_len,
+                              int32_t causal, float scale, float k_scale, float v_scale,
+                              int64_t num_splits, void* workspace, int64_t workspace_bytes,
+                              int32_t phase, void* stream) {
+  if (!q || !k_cache || !v_cache || !out || !seq_lens || !block_table)
+    return fail(MX_STATUS_NULL_POINTER,
+                "q, k_cache, v_cache, out, seq_lens and block_table must be non-NULL");
+  if (!std::isfinite(k_scale) || !std::isfinite(v_scale))
+    return fail(MX_STATUS_INVALID_ARGUMENT, "k_scale and v_scale must be finite");
+  if (!std::isfinite(scale * k_scale))
+    return fail(MX_STATUS_INVALID_ARGUMENT, "scale * k_scale must be finite");
+  KvFormat kv;
+  kv.fp8 = true;
+  kv.k_scale = k_scale;
+  kv.v_scale = v_scale;
+  return decode_impl(q, k_cache, v_cache, out, nullptr, nullptr, seq_lens, block_table, batch,
+                     seqlen_q, num_heads, num_kv_heads, head_dim, page_size, num_pages,
+                     max_pages_per_seq, max_seq_len, causal, scale, num_splits, workspace,
+                     workspace_bytes, phase, stream, kv);
 }
 
 int mx_paged_gqa_decode_partial(const void* q, const void* k_cache, const void* v_cache,

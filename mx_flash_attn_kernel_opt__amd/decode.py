@@ -92,12 +92,16 @@ def _query_shape(q: torch.Tensor) -> tuple[int, int, int, int]:
     return tuple(q.shape)
 
 
-def _check_decode_inputs(q, k_cache, v_cache, block_table, seq_lens):
-    """Validates the decode operands; returns (device, B, SQ, Hq, D, num_pages, P, Hkv)."""
+def _check_decode_inputs(q, k_cache, v_cache, block_table, seq_lens, allow_fp8=False):
+    """Validates the decode operands; returns (device, B, SQ, Hq, D, num_pages, P, Hkv).
+    With ``allow_fp8`` the caches may be float8_e4m3fn (both of them) instead of bf16."""
     _require(q.is_cuda, "q must be a device tensor")
     dev = q.device
-    for name, t, dt in (("q", q, torch.bfloat16), ("k_cache", k_cache, torch.bfloat16),
-                        ("v_cache", v_cache, torch.bfloat16),
+    kv_dt = torch.bfloat16
+    if allow_fp8 and k_cache.dtype == torch.float8_e4m3fn:
+        kv_dt = torch.float8_e4m3fn
+    for name, t, dt in (("q", q, torch.bfloat16), ("k_cache", k_cache, kv_dt),
+                        ("v_cache", v_cache, kv_dt),
                         ("block_table", block_table, torch.int32),
                         ("seq_lens", seq_lens, torch.int32)):
         _require(t.device == dev, f"{name} must be on {dev}")
@@ -127,17 +131,22 @@ def paged_gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
                      scale: float | None = None, *, out: torch.Tensor | None = None,
                      causal: bool = False, num_splits: int = 0, max_seq_len: int = 0,
                      workspace: torch.Tensor | None = None, phase: int = 0,
-                     stream=None) -> torch.Tensor:
+                     stream=None, k_scale: float = 1.0, v_scale: float = 1.0) -> torch.Tensor:
     """out[b, i, h] = softmax(q[b, i, h] . K_b^T * scale) . V_b over the first seq_lens[b]
     tokens (with ``causal``, query token i of seqlen_q sees keys t < L - seqlen_q + i + 1).
 
     q: [B, Hq, D] (one query token) or [B, seqlen_q, Hq, D] bf16; k_cache / v_cache:
-    [num_pages, page_size, Hkv, D] bf16; block_table: [B, max_pages] int32; seq_lens: [B] int32;
-    all on one GPU, contiguous.  ``scale`` defaults to 1/sqrt(D) (reference
-    submission_clean.cu:451).
+    [num_pages, page_size, Hkv, D] bf16, or float8_e4m3fn with per-tensor scales (the keys and
+    values are ``k_scale`` / ``v_scale`` times the stored ones; 1 for bf16 caches);
+    block_table: [B, max_pages] int32; seq_lens: [B] int32; all on one GPU, contiguous.
+    ``scale`` defaults to 1/sqrt(D) (reference submission_clean.cu:451).
     """
     dev, B, SQ, Hq, D, num_pages, P, Hkv = _check_decode_inputs(q, k_cache, v_cache,
-                                                                block_table, seq_lens)
+                                                                block_table, seq_lens,
+                                                                allow_fp8=True)
+    fp8 = k_cache.dtype == torch.float8_e4m3fn
+    _require(fp8 or (k_scale == 1.0 and v_scale == 1.0),
+             "k_scale / v_scale apply to float8_e4m3fn caches only")
     if out is None:
         out = torch.empty_like(q)
     else:
@@ -148,11 +157,18 @@ def paged_gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     ws_bytes = _workspace_bytes(workspace, dev)
     lib = _lib.load()
     with torch.cuda.device(dev):
-        st = lib.mx_paged_gqa_decode(
-            _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(seq_lens),
-            _ptr(block_table), B, SQ, Hq, Hkv, D, P, num_pages, block_table.shape[1],
-            max_seq_len, int(bool(causal)), float(scale), num_splits, _ptr(workspace), ws_bytes,
-            phase, _stream_handle(stream, dev))
+        if fp8:
+            st = lib.mx_paged_gqa_decode_fp8kv(
+                _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(seq_lens),
+                _ptr(block_table), B, SQ, Hq, Hkv, D, P, num_pages, block_table.shape[1],
+                max_seq_len, int(bool(causal)), float(scale), float(k_scale), float(v_scale),
+                num_splits, _ptr(workspace), ws_bytes, phase, _stream_handle(stream, dev))
+        else:
+            st = lib.mx_paged_gqa_decode(
+                _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(seq_lens),
+                _ptr(block_table), B, SQ, Hq, Hkv, D, P, num_pages, block_table.shape[1],
+                max_seq_len, int(bool(causal)), float(scale), num_splits, _ptr(workspace),
+                ws_bytes, phase, _stream_handle(stream, dev))
     _lib.check(st)
     return out
 

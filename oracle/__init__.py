@@ -31,6 +31,12 @@ Pinning (what each function is checked against, in tests/test_oracle.py):
                           the paged K/V append (flash_attn_with_kvcache's k / v); pinned by
                           the round trip through the decode oracle against plain attention
                           over the concatenated keys, computed by torch's SDPA.
+  paged_decode_fp8_reference
+                          the decode over a float8_e4m3fn cache with per-tensor scales
+                          (beyond the reference, whose cache is bf16): the decode oracle on
+                          caches dequantized by torch's e4m3fn conversion; pinned by known
+                          e4m3fn codes (1, 448, the smallest subnormal, -0, NaN), by agreement
+                          with the bf16 oracle on the same values and by scale linearity.
 No reference-held fixtures exist for this path (the reference checks live against the absent
 third-party flash_attn_with_kvcache, verify_real.py:40-41), so parity with that library is
 unpinned; the task.md:85-96 example is kept as a shape fixture under tests/golden/.
@@ -38,10 +44,12 @@ unpinned; the task.md:85-96 example is kept as a shape fixture under tests/golde
 
 from .paged_attention import (  # noqa: F401
     combine_partials,
+    fp8_dequantize,
     kv_bytes,
     lse_merge_reference,
     paged_decode_append_reference,
     paged_decode_fp64,
+    paged_decode_fp8_reference,
     paged_decode_partial_reference,
     paged_decode_reference,
     paged_kv_append_reference,

@@ -86,6 +86,24 @@ def paged_decode_reference(q, k_cache, v_cache, block_table, seq_lens, scale=Non
     return out if q.dim() == 4 else out[:, 0]
 
 
+def fp8_dequantize(cache: torch.Tensor, scale: float) -> torch.Tensor:
+    """fp32 values of a float8_e4m3fn cache (OCP e4m3fn, torch's conversion) times its
+    per-tensor scale."""
+    assert cache.dtype == torch.float8_e4m3fn
+    return cache.float() * float(scale)
+
+
+def paged_decode_fp8_reference(q, k_cache, v_cache, block_table, seq_lens, scale=None,
+                               k_scale: float = 1.0, v_scale: float = 1.0,
+                               causal: bool = False) -> torch.Tensor:
+    """The decode over an fp8 K/V cache: paged_decode_reference on the dequantized caches
+    (keys k_scale times the stored e4m3fn values, values v_scale times theirs), the semantics
+    of a per-tensor-scaled fp8 KV cache."""
+    return paged_decode_reference(q, fp8_dequantize(k_cache, k_scale),
+                                  fp8_dequantize(v_cache, v_scale), block_table, seq_lens,
+                                  scale, causal=causal)
+
+
 def paged_decode_fp64(q, k_cache, v_cache, block_table, seq_lens, scale=None,
                       causal: bool = False) -> np.ndarray:
     """fp64 numpy brute force, token by token (tiny shapes only).  Returns q's shape:

@@ -435,3 +435,37 @@ def _decode_append(**over):
 def test_append_and_attend_rejects_invalid_arguments(over, status):
     assert _decode_append(**over) == status
     assert _lib.load().mx_last_error()
+
+
+# ------------------------------------------------------------------------------------------
+# fp8 K/V cache: validation (no HIP call is reached on these paths)
+# ------------------------------------------------------------------------------------------
+
+def _decode_fp8(**over):
+    a = dict(q=FAKE, k=FAKE, v=FAKE, out=FAKE, lens=FAKE, table=FAKE, B=2, SQ=1, Hq=32, Hkv=8,
+             D=128, P=16, pages=64, max_pages=32, max_seq=0, causal=0, scale=0.088,
+             k_scale=0.5, v_scale=2.0, ns=2, ws=FAKE, ws_bytes=1 << 30, phase=0, stream=None)
+    a.update(over)
+    return _lib.load().mx_paged_gqa_decode_fp8kv(
+        a["q"], a["k"], a["v"], a["out"], a["lens"], a["table"], a["B"], a["SQ"], a["Hq"],
+        a["Hkv"], a["D"], a["P"], a["pages"], a["max_pages"], a["max_seq"], a["causal"],
+        a["scale"], a["k_scale"], a["v_scale"], a["ns"], a["ws"], a["ws_bytes"], a["phase"],
+        a["stream"])
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(q=None), _lib.MX_STATUS_NULL_POINTER),
+    (dict(k=None), _lib.MX_STATUS_NULL_POINTER),
+    (dict(table=None), _lib.MX_STATUS_NULL_POINTER),
+    (dict(k_scale=float("nan")), _lib.MX_STATUS_INVALID_ARGUMENT),
+    (dict(v_scale=float("inf")), _lib.MX_STATUS_INVALID_ARGUMENT),
+    (dict(scale=1e30, k_scale=1e30), _lib.MX_STATUS_INVALID_ARGUMENT),
+    (dict(v=ctypes.c_void_p(0x1008)), _lib.MX_STATUS_INVALID_ARGUMENT),
+    (dict(Hq=30), _lib.MX_STATUS_INVALID_SHAPE),
+    (dict(D=96), _lib.MX_STATUS_UNSUPPORTED),
+    (dict(causal=3), _lib.MX_STATUS_INVALID_ARGUMENT),
+    (dict(ws_bytes=100), _lib.MX_STATUS_WORKSPACE_TOO_SMALL),
+])
+def test_fp8_decode_rejects_invalid_arguments(over, status):
+    assert _decode_fp8(**over) == status
+    assert _lib.load().mx_last_status() == status

@@ -588,3 +588,61 @@ def test_append_and_attend_is_masked_attention_over_the_concatenated_keys(sq, ca
         exp = F.scaled_dot_product_attention(q[b].double().permute(1, 0, 2), kk, vv,
                                              attn_mask=mask)          # [Hq, sq, D]
         assert torch.allclose(out[b].double(), exp.permute(1, 0, 2), atol=1e-5), b
+
+
+# ------------------------------------------------------------------------------------------
+# fp8 (OCP e4m3fn) K/V cache oracle
+# ------------------------------------------------------------------------------------------
+
+def test_fp8_dequantize_known_codes():
+    """torch's e4m3fn conversion, which the fp8 oracle relies on, on codes whose values the
+    OCP format fixes: 0x38 = 1, 0x7e = 448 (largest finite), 0x01 = 2^-9 (smallest subnormal),
+    0x08 = 2^-6 (smallest normal), 0x80 = -0, 0x7f = NaN, and the scale multiplies."""
+    from oracle import fp8_dequantize
+    codes = torch.tensor([0x38, 0x7E, 0x01, 0x08, 0x80, 0x7F, 0xB8, 0x3C], dtype=torch.uint8)
+    x = fp8_dequantize(codes.view(torch.float8_e4m3fn), 1.0)
+    assert x[0] == 1.0 and x[1] == 448.0 and x[2] == 2.0 ** -9 and x[3] == 2.0 ** -6
+    assert x[4] == 0.0 and math.copysign(1.0, x[4].item()) == -1.0
+    assert torch.isnan(x[5]) and x[6] == -1.0 and x[7] == 1.5
+    assert torch.equal(fp8_dequantize(codes[:4].view(torch.float8_e4m3fn), 0.25), x[:4] * 0.25)
+
+
+def _fp8_case(seed, lens, Hq=8, Hkv=2, D=64, P=16):
+    g = torch.Generator().manual_seed(seed)
+    B = len(lens)
+    width = max(1, -(-max(lens) // P))
+    pool = B * width + 3
+    k8 = (torch.randn(pool, P, Hkv, D, generator=g) * 3).to(torch.float8_e4m3fn)
+    v8 = (torch.randn(pool, P, Hkv, D, generator=g) * 3).to(torch.float8_e4m3fn)
+    q = torch.randn(B, Hq, D, generator=g).to(torch.bfloat16)
+    table = torch.randperm(pool, generator=g)[: B * width].to(torch.int32).view(B, width)
+    return q, k8, v8, table, torch.tensor(lens, dtype=torch.int32)
+
+
+def test_fp8_oracle_equals_the_bf16_oracle_on_the_same_values():
+    """Every e4m3fn value is a bf16 value, so the fp8 oracle with unit scales must equal the
+    bf16 oracle on the bf16 copy of the caches exactly, and with scales (powers of two keep the
+    products exact) the bf16 oracle on pre-scaled copies."""
+    from oracle import paged_decode_fp8_reference
+    q, k8, v8, table, lens = _fp8_case(3, [1, 17, 40])
+    kb, vb = k8.float().to(torch.bfloat16), v8.float().to(torch.bfloat16)
+    assert torch.equal(kb.float(), k8.float()) and torch.equal(vb.float(), v8.float())
+    a = paged_decode_fp8_reference(q, k8, v8, table, lens)
+    b = paged_decode_reference(q, kb, vb, table, lens)
+    assert torch.equal(a, b)
+    a2 = paged_decode_fp8_reference(q, k8, v8, table, lens, k_scale=0.5, v_scale=4.0)
+    b2 = paged_decode_reference(q, (kb.float() * 0.5).to(torch.bfloat16),
+                                (vb.float() * 4.0).to(torch.bfloat16), table, lens)
+    assert torch.allclose(a2, b2, atol=1e-5, rtol=1e-5)
+
+
+def test_fp8_oracle_scales_are_not_swapped():
+    """A planted mistake (k and v scales swapped) changes the result: k_scale sharpens the
+    softmax, v_scale multiplies the output."""
+    from oracle import paged_decode_fp8_reference
+    q, k8, v8, table, lens = _fp8_case(4, [30, 50])
+    a = paged_decode_fp8_reference(q, k8, v8, table, lens, k_scale=2.0, v_scale=0.5)
+    swapped = paged_decode_fp8_reference(q, k8, v8, table, lens, k_scale=0.5, v_scale=2.0)
+    assert not torch.allclose(a, swapped, atol=1e-3)
+    unit = paged_decode_fp8_reference(q, k8, v8, table, lens, k_scale=2.0, v_scale=1.0)
+    assert torch.allclose(a, unit * 0.5, atol=1e-6, rtol=1e-6)
