@@ -85,7 +85,8 @@ def time_workload(inp: W.DecodeInputs, steps: int, warmup: int, num_splits: int 
     With `graph`, also time the same calls captured in a HIP graph and replayed."""
     spec = inp.spec
     stream = torch.cuda.current_stream()
-    nbytes = inp.kv_bytes()
+    fp8 = inp.k_cache.dtype == torch.float8_e4m3fn
+    nbytes = inp.kv_bytes() // (2 if fp8 else 1)
     # Rotate distinct copies of the KV pool when one would fit in the 256 MB MALL: enough that
     # the K/V bytes of the rotation exceed three MALLs, so a call never finds its pages there.
     copies = (1 if nbytes >= 3 * MALL_BYTES
@@ -93,7 +94,8 @@ def time_workload(inp: W.DecodeInputs, steps: int, warmup: int, num_splits: int 
     pools = [(inp.k_cache, inp.v_cache)] + [(inp.k_cache.clone(), inp.v_cache.clone())
                                             for _ in range(copies - 1)]
     plan = pkg.plan(spec.batch, spec.num_heads, spec.num_kv_heads, spec.head_dim,
-                    spec.page_size, spec.max_pages, 0, num_splits, seqlen_q=spec.seqlen_q)
+                    spec.page_size, spec.max_pages, 0, num_splits, seqlen_q=spec.seqlen_q,
+                    fp8=fp8)
     ws = pkg.make_workspace(plan["workspace_bytes"], inp.device)
     out = torch.empty_like(inp.q)
     calls = [pkg.BoundDecode(inp.q, k, v, inp.block_table, inp.seq_lens, inp.scale, out=out,
@@ -145,6 +147,7 @@ def time_workload(inp: W.DecodeInputs, steps: int, warmup: int, num_splits: int 
     kern_mean = statistics.fmean(kern_us)
     return {
         "nbytes": nbytes,
+        "fp8": fp8,
         "plan": plan,
         "ms_per_step": ms_per_step,
         "wall_ms_per_step": wall_ms_step,
@@ -453,17 +456,19 @@ def c500_suite(mult: int = 10, seed: int = 42) -> list[dict]:
 
 
 def cpu_baseline(inp: W.DecodeInputs, budget_s: float) -> dict:
-    """fp32 oracle (the reference CPU path restated) on a bounded sample of sequences."""
-    from oracle import paged_decode_reference
+    """fp32 oracle (the reference CPU path restated) on a bounded sample of sequences; for an
+    fp8 cache, the oracle's dequantizing decode over the fp8 bytes."""
+    from oracle import paged_decode_fp8_reference, paged_decode_reference
 
     threads = torch.get_num_threads()
     B = inp.spec.batch
     order = torch.randperm(B, generator=torch.Generator().manual_seed(0)).tolist()
     subs = []
+    fp8 = inp.k_cache.dtype == torch.float8_e4m3fn
+    ref = paged_decode_fp8_reference if fp8 else paged_decode_reference
 
     def run(sub):
-        paged_decode_reference(sub.q, sub.k_cache, sub.v_cache, sub.block_table, sub.seq_lens,
-                               sub.scale)
+        ref(sub.q, sub.k_cache, sub.v_cache, sub.block_table, sub.seq_lens, sub.scale)
 
     # Sample: sequences in a fixed random order until one pass takes about a third of the
     # budget (one pass also warms up); then 3 timed passes over that sample, median reported.
@@ -476,7 +481,7 @@ def cpu_baseline(inp: W.DecodeInputs, budget_s: float) -> dict:
         subs.append(sub)
         if first >= budget_s / 3:
             break
-    nbytes = sum(sub.kv_bytes() for sub in subs)
+    nbytes = sum(sub.kv_bytes() for sub in subs) // (2 if fp8 else 1)
     passes = []
     for _ in range(3):
         t0 = time.perf_counter()
@@ -490,7 +495,8 @@ def cpu_baseline(inp: W.DecodeInputs, budget_s: float) -> dict:
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"{len(subs)} of {B} sequences of {inp.spec.name}, fp32 torch oracle "
+        "sample": (f"{len(subs)} of {B} sequences of {inp.spec.name}"
+                   f"{' (fp8 cache)' if fp8 else ''}, fp32 torch oracle "
                    f"(oracle/paged_attention.py), one sequence at a time; median of 3 passes "
                    f"of {per_pass:.2f} s after a warm-up pass; host {_cpu_model()}, "
                    f"os.cpu_count()={os.cpu_count()}, torch threads={threads}"),
@@ -514,13 +520,16 @@ def result_line(args, spec, r, cpu=None) -> dict:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) bf16 q/K/V, shuffled block table)",
+        "data": ("synthetic (seeded N(0,1) bf16 q/K/V, shuffled block table)" if not r["fp8"]
+                 else "synthetic (seeded N(0,1) bf16 q, K/V rounded to e4m3fn, shuffled block "
+                      "table)"),
         "config": {
             "workload": spec.name,
             "batch": spec.batch, "num_heads": spec.num_heads,
             "num_kv_heads": spec.num_kv_heads, "head_dim": spec.head_dim,
             "page_size": spec.page_size, "max_pages": spec.max_pages,
             "seq_lens": spec.seq_lens, "seq_args": list(spec.seq_args),
+            "kv_dtype": "fp8_e4m3fn" if r["fp8"] else "bf16",
             "kv_bytes": r["nbytes"], "schedule": r["plan"]["schedule"],
             "workgroups": r["plan"]["workgroups"], "splits": r["plan"]["splits"],
             "tokens_per_split": r["plan"]["tokens_per_split"], "kv_pools": r["pools"],
@@ -534,7 +543,8 @@ def result_line(args, spec, r, cpu=None) -> dict:
             "unit": "GB/s",
             "frac": round(frac, 4),
             "traffic": _traffic_from_profile(
-                "balanced" if r["plan"]["schedule"] == "balanced" else "splitkv", spec.name),
+                "balanced" if r["plan"]["schedule"] == "balanced" else "splitkv",
+                spec.name + ("_fp8" if r["fp8"] else "")),
             "kernel_us_mean": round(r["kernel_us_mean"], 2),
             "kernel_us_median": round(r["kernel_us_median"], 2),
         },
@@ -577,6 +587,10 @@ def main(argv=None) -> int:
     ap.add_argument("--shards", type=int, default=0,
                     help="also time the per-GPU pieces of the workload's decode sharded over N "
                          "GPUs' pages (partial decode per shard + merge), on this one GPU")
+    ap.add_argument("--kv-dtype", choices=["bf16", "fp8"], default="bf16",
+                    help="fp8: the same workload with K/V rounded to an e4m3fn cache (unit "
+                         "scales), decoded by mx_paged_gqa_decode_fp8kv; KV bytes are the fp8 "
+                         "bytes")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after timing, run 5 plain 1 GiB device copies (torch copy_) so a "
                          "rocprofv3 --pmc pass can scale FETCH_SIZE/WRITE_SIZE by a kernel of "
@@ -620,6 +634,10 @@ def main(argv=None) -> int:
 
     spec = W.get_spec(args.workload)
     inp = W.make_inputs(spec, seed=args.seed, device="cuda")
+    if args.kv_dtype == "fp8":
+        inp.k_cache = inp.k_cache.to(torch.float8_e4m3fn)
+        inp.v_cache = inp.v_cache.to(torch.float8_e4m3fn)
+        torch.cuda.empty_cache()
     r = time_workload(inp, args.steps, args.warmup, args.num_splits, graph=args.graph)
     cpu = None if args.no_cpu_baseline else cpu_baseline(inp, args.cpu_budget)
     line = result_line(args, spec, r, cpu)

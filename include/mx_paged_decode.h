@@ -135,6 +135,11 @@ int mx_paged_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
  * The kernels read half the bytes of a bf16 cache and widen the values to bf16 in registers
  * (exact: every e4m3fn value is a bf16 value) before the same MFMA path.  k_scale and v_scale
  * must be finite.
+ * With head_dim 64, an even num_kv_heads and seqlen_q * (num_heads / num_kv_heads) <= 16, the
+ * kernels read adjacent KV heads in pairs as one head of dim 128 (a 64-dim fp8 row is half a
+ * 128-byte line; unpaired, each line would be fetched once per head).  The workspace size and
+ * plan of this call: mx_paged_gqa_decode_workspace_size (which covers both cache formats) and
+ * mx_paged_gqa_decode_plan_fp8kv.
  * No counterpart in the reference, whose cache is bf16 only; it is the same operator on a
  * narrower cache format.
  */
@@ -199,9 +204,18 @@ int mx_paged_gqa_decode_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads,
                              int64_t* tokens_per_split_out, int64_t* workgroups_out,
                              int64_t* workspace_bytes_out);
 
+/* The plan of the same call through mx_paged_gqa_decode_fp8kv (arguments and outputs as
+ * mx_paged_gqa_decode_plan's).  No counterpart in the reference (bf16 caches only). */
+int mx_paged_gqa_decode_plan_fp8kv(int64_t batch, int64_t seqlen_q, int64_t num_heads,
+                                   int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                                   int64_t max_pages_per_seq, int64_t max_seq_len,
+                                   int64_t num_splits, int64_t num_cus, int64_t* schedule_out,
+                                   int64_t* splits_out, int64_t* tokens_per_split_out,
+                                   int64_t* workgroups_out, int64_t* workspace_bytes_out);
+
 /* Workspace bytes a call needs (replaces the grow-only sizing of submission_clean.cu:463,
- * 478-491); negative MX_STATUS_* on invalid arguments.  Queries the current device's CU count
- * when num_splits == 0. */
+ * 478-491), on a bf16 or an fp8 cache; negative MX_STATUS_* on invalid arguments.  Queries the
+ * current device's CU count when num_splits == 0. */
 int64_t mx_paged_gqa_decode_workspace_size(int64_t batch, int64_t seqlen_q, int64_t num_heads,
                                            int64_t num_kv_heads, int64_t head_dim,
                                            int64_t page_size, int64_t max_pages_per_seq,

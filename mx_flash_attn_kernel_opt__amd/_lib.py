@@ -65,6 +65,7 @@ SIGNATURES = {
     ),
     "mx_lse_merge": (ctypes.c_int, [_VP, _VP, _I64, _I64, _I64, _VP, _VP]),
     "mx_paged_gqa_decode_plan": (ctypes.c_int, [_I64] * 10 + [_P64] * 5),
+    "mx_paged_gqa_decode_plan_fp8kv": (ctypes.c_int, [_I64] * 10 + [_P64] * 5),
     "mx_paged_gqa_decode_workspace_size": (ctypes.c_int64, [_I64] * 9),
     "mx_paged_kv_append": (ctypes.c_int, [_VP] * 6 + [_I64] * 7 + [_VP, _VP]),
     "mx_paged_gqa_decode_append": (

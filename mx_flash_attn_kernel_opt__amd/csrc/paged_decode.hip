@@ -487,6 +487,12 @@ struct MainShape {
   int num_kv_heads;
   int group;
   uint32_t group_magic;  // floor(2^32 / group) + 1 (0 when group == 1): r / group by mul-high
+  // Paired heads (head_dim 128 kernels only): 0, or the query group of the stored heads when each
+  // KV head of the kernel is two adjacent stored heads of dim 64.  A token's rows of the two are
+  // contiguous, so K and V read as one head of dim 128.  Rows of the first stored head carry their
+  // query in dims 0..63 of the operand and zeros above, rows of the second in dims 64..127, so
+  // each row's scores use its own head's keys; of its PV output each row keeps its own half.
+  int pair_group;
   int seqlen_q;          // query tokens per sequence
   int causal;            // row t sees keys [0, L - seqlen_q + t + 1) (bottom-right aligned)
   int rows;              // seqlen_q * group
@@ -585,6 +591,21 @@ __device__ __forceinline__ void load_q(bf16x8 (&qop)[D / 32], const uint16_t* q,
   const int g4 = lane >> 4;
   const int r = tile * 16 + (lane & 15);
   const bool live = r < sh.rows;
+  if constexpr (D == 128) {
+    if (sh.pair_group > 0) {  // q rows of 64 dims, placed in the row's half (MainShape)
+      const int rr = live ? r : 0;
+      const bool hi = rr - row_token(rr, sh) * sh.group >= sh.pair_group;
+      const uint16_t* qp = q + (row_base(b, kv, sh) + row_offset(rr, sh)) * (D / 2) + 8 * g4;
+#pragma unroll
+      for (int i = 0; i < D / 32; ++i) {
+        u32x4 x = {0, 0, 0, 0};
+        if (live && (i >= D / 64) == hi)
+          x = *reinterpret_cast<const u32x4*>(qp + 32 * (i % (D / 64)));
+        qop[i] = __builtin_bit_cast(bf16x8, x);
+      }
+      return;
+    }
+  }
   const uint16_t* qp = q + (row_base(b, kv, sh) + (live ? row_offset(r, sh) : 0)) * D + 8 * g4;
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) {
@@ -832,15 +853,27 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 // Final output of dims d..d+3 of query row `row` with log2-sum-exp lse2: bf16 into out, or, for
 // partial outputs, fp32 into sh.o_out and (once per row) the natural-log sum-exp into sh.lse_out.
+// With paired heads (MainShape::pair_group) rows are 64 dims and only the row's own half of
+// the kernel's 128 is written.
 template <int D>
 __device__ __forceinline__ void store_row4(uint16_t* out, const MainShape& sh, int64_t row, int d,
                                            f32x4 o, float lse2) {
+  int64_t at = row * D + d;
+  bool first = d == 0;
+  if constexpr (D == 128) {
+    if (sh.pair_group > 0) {
+      const int hi = ((uint32_t)row % (uint32_t)sh.num_heads / (uint32_t)sh.pair_group) & 1;
+      if ((d >= D / 2) != (hi != 0)) return;
+      at = row * (D / 2) + d - hi * (D / 2);
+      first = d == hi * (D / 2);
+    }
+  }
   if (sh.o_out == nullptr) {
-    store_bf16x4(out + row * D + d, o);
+    store_bf16x4(out + at, o);
     return;
   }
-  *reinterpret_cast<f32x4*>(sh.o_out + row * D + d) = o;
-  if (d == 0) sh.lse_out[row] = lse2 * kLn2;
+  *reinterpret_cast<f32x4*>(sh.o_out + at) = o;
+  if (first) sh.lse_out[row] = lse2 * kLn2;
 }
 
 // Row group g of a KV head: KT tiles of 16 rows, rows g*16*KT + t*16 + r16.  Loads the query
@@ -1725,21 +1758,31 @@ __device__ __forceinline__ float merge_row(float (&acc)[D / 64], const float* __
 }
 
 // Writes a merged row (log2-sum-exp lse): bf16 to out, or (partial outputs) fp32 to o_out and
-// the natural-log sum-exp to lse_out.
+// the natural-log sum-exp to lse_out.  half >= 0 (paired heads, MainShape::pair_group): the
+// row is 64 dims, taken from half `half` of the D merged ones.
 template <int D>
 __device__ __forceinline__ void store_merged_row(const float (&acc)[D / 64], float lse,
                                                  uint16_t* __restrict__ out,
                                                  float* __restrict__ o_out,
                                                  float* __restrict__ lse_out, int64_t row,
-                                                 int lane) {
+                                                 int lane, int half = -1) {
   constexpr int E = D / 64;
+  int64_t at = row * D + E * lane;
+  bool first = lane == 0;
+  if constexpr (D == 128) {
+    if (half >= 0) {
+      if ((E * lane >= D / 2) != (half == 1)) return;
+      at = row * (D / 2) + E * lane - half * (D / 2);
+      first = E * lane == half * (D / 2);
+    }
+  }
   if (o_out != nullptr) {
 #pragma unroll
-    for (int e = 0; e < E; ++e) o_out[row * D + E * lane + e] = acc[e];
-    if (lane == 0) lse_out[row] = lse * kLn2;
+    for (int e = 0; e < E; ++e) o_out[at + e] = acc[e];
+    if (first) lse_out[row] = lse * kLn2;
     return;
   }
-  uint16_t* op = out + row * D + E * lane;
+  uint16_t* op = out + at;
   if constexpr (E == 1) {
     op[0] = __builtin_bit_cast(uint16_t, (__bf16)acc[0]);
   } else if constexpr (E == 2) {
@@ -1757,7 +1800,7 @@ __global__ __launch_bounds__(64) void mx_paged_decode_combine(
     const float* __restrict__ part_o, const float* __restrict__ part_lse,
     const int32_t* __restrict__ seq_lens, uint16_t* __restrict__ out, float* __restrict__ o_out,
     float* __restrict__ lse_out, int num_heads, int seqlen_q, int num_splits,
-    int tokens_per_split, int cap_tokens, int appended, int new_tokens) {
+    int tokens_per_split, int cap_tokens, int appended, int new_tokens, int pair_group) {
   const int h = blockIdx.x;
   const int bt = blockIdx.y;  // sequence * seqlen_q + query token
   const int b = bt / seqlen_q;
@@ -1771,7 +1814,8 @@ __global__ __launch_bounds__(64) void mx_paged_decode_combine(
   float acc[D / 64];
   const float lse = merge_row<D>(acc, part_lse + row * num_splits, 1, 1.0f,
                                  part_o + row * num_splits * D, D, nsv, lane);
-  store_merged_row<D>(acc, lse, out, o_out, lse_out, row, lane);
+  store_merged_row<D>(acc, lse, out, o_out, lse_out, row, lane,
+                      pair_group > 0 ? (h / pair_group) & 1 : -1);
 }
 
 // mx_lse_merge: rows merged over `parts` gathered partials, part-major ([parts, rows, D] and
@@ -2112,9 +2156,36 @@ struct KvFormat {
   float v_scale = 1.0f;
 };
 
+// Whether bf16 caches of head_dim 64 also run as paired heads (KernelHeads).  Off: a bf16 row of
+// 64 dims is a whole line already, and pairing measured 171.1 -> 168.8 us on B=128, Hkv=4,
+// L=8192, within the spread of repeated runs.
+#ifndef MX_PAIR_BF16
+#define MX_PAIR_BF16 0
+#endif
+
+// KV heads as the kernels see them.  Stored heads of dim 64 run in adjacent pairs as kernel heads
+// of dim 128 (MainShape::pair_group) when a head's query rows fit one 16-row tile, so that a
+// pair is still one pass over its K/V.  For fp8 caches this is what makes the reads whole: an
+// fp8 row of 64 dims is half a 128-byte line, which the workgroups of the two unpaired heads
+// each fetch in full (FETCH_SIZE read 2.0x the cache bytes).
+struct KernelHeads {
+  int64_t kv_heads;
+  int64_t head_dim;
+  int pair_group;  // 0: heads as stored; else the stored heads' query group
+};
+
+KernelHeads kernel_heads(int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads,
+                         int64_t head_dim, bool fp8) {
+  const bool pair = (fp8 || MX_PAIR_BF16) && head_dim == 64 && num_kv_heads >= 2 &&
+                    num_kv_heads % 2 == 0 && num_heads % num_kv_heads == 0 && seqlen_q >= 1 &&
+                    seqlen_q <= 16 && seqlen_q * (num_heads / num_kv_heads) <= 16;
+  if (!pair) return {num_kv_heads, head_dim, 0};
+  return {num_kv_heads / 2, 128, (int)(num_heads / num_kv_heads)};
+}
+
 // Register ring depth of the fp8 kernels (an fp8 chunk takes half the registers of a bf16 one).
 // (A/B on 512 MB fp8 caches, chunks per ring 2/3/4/6: D=64 173.6/174.7/183.0/186.2 us, D=128
-// config-2 shape 95.8/93.2/95.7/96.4 us, D=256 1/2/3 chunks 93.3/95.0/104.1 us.)
+// config-2 shape 95.8/93.2/95.7/96.4 us, D=256 1/2/3/6 chunks 94.5/93.3-96.7/94.9/104.1 us.)
 #ifndef MX_NBUF8_D64
 #define MX_NBUF8_D64 2
 #endif
@@ -2135,7 +2206,7 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
                   int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads, int64_t page_size,
                   int64_t num_pages, int64_t max_pages, float scale, char* ws, int32_t phase,
                   float* o_out, float* lse_out, const AppendArgs& app, const KvFormat& kv,
-                  hipStream_t stream) {
+                  int pair_group, hipStream_t stream) {
   constexpr int kNW = waves_per_group<D>();
   constexpr int kNBUF = ring_depth<D>();
   constexpr int kNBUF8 = ring_depth_fp8<D>();
@@ -2146,6 +2217,8 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   sh.num_kv_heads = (int)num_kv_heads;
   sh.group = (int)(num_heads / num_kv_heads);
   sh.group_magic = sh.group == 1 ? 0u : (uint32_t)((1ull << 32) / (uint64_t)sh.group + 1);
+  if (pair_group > 0 && D != 128) return hipErrorInvalidValue;
+  sh.pair_group = pair_group;
   sh.seqlen_q = (int)seqlen_q;
   sh.causal = kCausal ? 1 : 0;
   sh.rows = (int)plan.rows;
@@ -2235,7 +2308,7 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
     hipLaunchKernelGGL(mx_paged_decode_combine<D>, grid, dim3(64), 0, stream, part_o, part_lse,
                        seq_lens, static_cast<uint16_t*>(out), o_out, lse_out, (int)num_heads,
                        (int)seqlen_q, (int)plan.splits, (int)plan.tokens_per_split,
-                       (int)plan.cap_tokens, app.appended, app.new_tokens);
+                       (int)plan.cap_tokens, app.appended, app.new_tokens, pair_group);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -2250,14 +2323,16 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
 
 extern "C" {
 
-int mx_paged_gqa_decode_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads,
-                             int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
-                             int64_t max_pages_per_seq, int64_t max_seq_len, int64_t num_splits,
-                             int64_t num_cus, int64_t* schedule_out, int64_t* splits_out,
-                             int64_t* tokens_per_split_out, int64_t* workgroups_out,
-                             int64_t* workspace_bytes_out) {
+// The plan of a bf16 (fp8 = false) or fp8 cache call.
+static int report_plan(bool fp8, int64_t batch, int64_t seqlen_q, int64_t num_heads,
+                       int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                       int64_t max_pages_per_seq, int64_t max_seq_len, int64_t num_splits,
+                       int64_t num_cus, int64_t* schedule_out, int64_t* splits_out,
+                       int64_t* tokens_per_split_out, int64_t* workgroups_out,
+                       int64_t* workspace_bytes_out) {
   Plan plan;
-  const int st = make_plan(batch, seqlen_q, num_heads, num_kv_heads, head_dim, page_size,
+  const KernelHeads kh = kernel_heads(seqlen_q, num_heads, num_kv_heads, head_dim, fp8);
+  const int st = make_plan(batch, seqlen_q, num_heads, kh.kv_heads, kh.head_dim, page_size,
                            max_pages_per_seq, max_seq_len, num_splits, num_cus, &plan);
   if (st != MX_STATUS_OK) return st;
   if (schedule_out) *schedule_out = plan.schedule;
@@ -2266,21 +2341,49 @@ int mx_paged_gqa_decode_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads,
   if (workgroups_out)
     *workgroups_out = plan.schedule == MX_SCHEDULE_BALANCED
                           ? plan.groups
-                          : batch * num_kv_heads * plan.row_tiles * plan.splits;
+                          : batch * kh.kv_heads * plan.row_tiles * plan.splits;
   if (workspace_bytes_out) *workspace_bytes_out = plan.workspace_bytes;
   return ok();
+}
+
+int mx_paged_gqa_decode_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads,
+                             int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                             int64_t max_pages_per_seq, int64_t max_seq_len, int64_t num_splits,
+                             int64_t num_cus, int64_t* schedule_out, int64_t* splits_out,
+                             int64_t* tokens_per_split_out, int64_t* workgroups_out,
+                             int64_t* workspace_bytes_out) {
+  return report_plan(false, batch, seqlen_q, num_heads, num_kv_heads, head_dim, page_size,
+                     max_pages_per_seq, max_seq_len, num_splits, num_cus, schedule_out,
+                     splits_out, tokens_per_split_out, workgroups_out, workspace_bytes_out);
+}
+
+int mx_paged_gqa_decode_plan_fp8kv(int64_t batch, int64_t seqlen_q, int64_t num_heads,
+                                   int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                                   int64_t max_pages_per_seq, int64_t max_seq_len,
+                                   int64_t num_splits, int64_t num_cus, int64_t* schedule_out,
+                                   int64_t* splits_out, int64_t* tokens_per_split_out,
+                                   int64_t* workgroups_out, int64_t* workspace_bytes_out) {
+  return report_plan(true, batch, seqlen_q, num_heads, num_kv_heads, head_dim, page_size,
+                     max_pages_per_seq, max_seq_len, num_splits, num_cus, schedule_out,
+                     splits_out, tokens_per_split_out, workgroups_out, workspace_bytes_out);
 }
 
 int64_t mx_paged_gqa_decode_workspace_size(int64_t batch, int64_t seqlen_q, int64_t num_heads,
                                            int64_t num_kv_heads, int64_t head_dim,
                                            int64_t page_size, int64_t max_pages_per_seq,
                                            int64_t max_seq_len, int64_t num_splits) {
-  Plan plan;
-  const int st = make_plan(batch, seqlen_q, num_heads, num_kv_heads, head_dim, page_size,
-                           max_pages_per_seq, max_seq_len, num_splits, 0, &plan);
-  if (st != MX_STATUS_OK) return st;
+  // The size covers the call on a bf16 and on an fp8 cache (whose kernel heads may differ).
+  int64_t bytes = 0;
+  for (const bool fp8 : {false, true}) {
+    Plan plan;
+    const KernelHeads kh = kernel_heads(seqlen_q, num_heads, num_kv_heads, head_dim, fp8);
+    const int st = make_plan(batch, seqlen_q, num_heads, kh.kv_heads, kh.head_dim, page_size,
+                             max_pages_per_seq, max_seq_len, num_splits, 0, &plan);
+    if (st != MX_STATUS_OK) return st;
+    bytes = std::max(bytes, plan.workspace_bytes);
+  }
   ok();
-  return plan.workspace_bytes;
+  return bytes;
 }
 
 }  // extern "C"
@@ -2326,7 +2429,7 @@ int run_decode(const Plan& plan, const void* q, const void* k_cache, const void*
                int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_pages,
                int64_t max_pages_per_seq, int32_t causal, float scale, void* workspace,
                int32_t phase, const AppendArgs& app, void* stream,
-               const KvFormat& kv = KvFormat{}) {
+               const KvFormat& kv = KvFormat{}, int pair_group = 0) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   hipError_t e;
@@ -2335,7 +2438,7 @@ int run_decode(const Plan& plan, const void* q, const void* k_cache, const void*
 #define MX_LAUNCH(DIM, CAUSAL, KT)                                                            \
   launch<DIM, CAUSAL, KT>(plan, q, k_cache, v_cache, out, seq_lens, block_table, batch, seqlen_q, \
                       num_heads, num_kv_heads, page_size, num_pages, max_pages_per_seq, scale, \
-                      ws, phase, o_out, lse_out, app, kv, s)
+                      ws, phase, o_out, lse_out, app, kv, pair_group, s)
   const bool pair = plan.tiles_per_group == 2;
   switch (head_dim) {
     case 64:
@@ -2366,14 +2469,16 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* o
                 void* workspace, int64_t workspace_bytes, int32_t phase, void* stream,
                 const KvFormat& kv = KvFormat{}) {
   Plan plan;
+  const KernelHeads kh = kernel_heads(seqlen_q, num_heads, num_kv_heads, head_dim, kv.fp8);
   const int st = prepare_decode(q, k_cache, v_cache, out, batch, seqlen_q, num_heads,
-                                num_kv_heads, head_dim, page_size, num_pages, max_pages_per_seq,
+                                kh.kv_heads, kh.head_dim, page_size, num_pages, max_pages_per_seq,
                                 max_seq_len, causal, scale, num_splits, &workspace,
                                 workspace_bytes, phase, &plan);
   if (st != MX_STATUS_OK) return st;
   return run_decode(plan, q, k_cache, v_cache, out, o_out, lse_out, seq_lens, block_table, batch,
-                    seqlen_q, num_heads, num_kv_heads, head_dim, page_size, num_pages,
-                    max_pages_per_seq, causal, scale, workspace, phase, AppendArgs{}, stream, kv);
+                    seqlen_q, num_heads, kh.kv_heads, kh.head_dim, page_size, num_pages,
+                    max_pages_per_seq, causal, scale, workspace, phase, AppendArgs{}, stream, kv,
+                    kh.pair_group);
 }
 
 // Argument checks of a paged K/V append (shared by mx_paged_kv_append and the fused
@@ -2617,14 +2722,15 @@ int mx_paged_gqa_decode_append(const void* q, const void* k_new, const void* v_n
   if (seqlen_new > INT32_MAX / 2)
     return fail(MX_STATUS_UNSUPPORTED, "seqlen_new must be < 2^30");
   Plan plan;
-  st = prepare_decode(q, k_cache, v_cache, out, batch, seqlen_q, num_heads, num_kv_heads,
-                      head_dim, page_size, num_pages, max_pages_per_seq, max_seq_len, causal,
+  const KernelHeads kh = kernel_heads(seqlen_q, num_heads, num_kv_heads, head_dim, false);
+  st = prepare_decode(q, k_cache, v_cache, out, batch, seqlen_q, num_heads, kh.kv_heads,
+                      kh.head_dim, page_size, num_pages, max_pages_per_seq, max_seq_len, causal,
                       scale, num_splits, &workspace, workspace_bytes, 0, &plan);
   if (st != MX_STATUS_OK) return st;
   AppendArgs app;
-  const bool lds_k = head_dim == 64    ? k_via_lds<64>()
-                     : head_dim == 128 ? k_via_lds<128>()
-                                       : k_via_lds<256>();
+  const bool lds_k = kh.head_dim == 64    ? k_via_lds<64>()
+                     : kh.head_dim == 128 ? k_via_lds<128>()
+                                          : k_via_lds<256>();
   if (seqlen_new >= 1 && seqlen_new <= kChunk && lds_k) {
     // One launch: the new keys are one extra chunk of each unit, written to the cache by the
     // wave that loads them.
@@ -2640,8 +2746,9 @@ int mx_paged_gqa_decode_append(const void* q, const void* k_new, const void* v_n
     app.appended = (int)seqlen_new;
   }
   return run_decode(plan, q, k_cache, v_cache, out, nullptr, nullptr, seq_lens, block_table,
-                    batch, seqlen_q, num_heads, num_kv_heads, head_dim, page_size, num_pages,
-                    max_pages_per_seq, causal, scale, workspace, 0, app, stream);
+                    batch, seqlen_q, num_heads, kh.kv_heads, kh.head_dim, page_size, num_pages,
+                    max_pages_per_seq, causal, scale, workspace, 0, app, stream, KvFormat{},
+                    kh.pair_group);
 }
 
 int mx_last_status(void) { return g_last_status; }

@@ -38,8 +38,9 @@ def _stream_handle(stream, device: torch.device) -> ctypes.c_void_p:
 
 def plan(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
          max_pages_per_seq: int, max_seq_len: int = 0, num_splits: int = 0,
-         num_cus: int = 0, seqlen_q: int = 1) -> dict:
-    """Split plan of a call (host only when ``num_cus`` > 0).
+         num_cus: int = 0, seqlen_q: int = 1, fp8: bool = False) -> dict:
+    """Split plan of a call (host only when ``num_cus`` > 0); ``fp8``: the call on an fp8
+    (e4m3fn) cache.
 
     Returns ``{"schedule", "splits", "tokens_per_split", "workgroups", "workspace_bytes",
     "launches"}`` (schedule: "split_grid" or "balanced"; launches: kernels a phase-0 call runs);
@@ -47,21 +48,17 @@ def plan(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, page_size
     """
     lib = _lib.load()
     sch, ns, tps, wgs, ws = (ctypes.c_int64() for _ in range(5))
-    st = lib.mx_paged_gqa_decode_plan(batch, seqlen_q, num_heads, num_kv_heads, head_dim,
-                                      page_size, max_pages_per_seq, max_seq_len, num_splits,
-                                      num_cus,
-                                      ctypes.byref(sch), ctypes.byref(ns), ctypes.byref(tps),
-                                      ctypes.byref(wgs), ctypes.byref(ws))
+    entry = lib.mx_paged_gqa_decode_plan_fp8kv if fp8 else lib.mx_paged_gqa_decode_plan
+    st = entry(batch, seqlen_q, num_heads, num_kv_heads, head_dim, page_size, max_pages_per_seq,
+               max_seq_len, num_splits, num_cus, ctypes.byref(sch), ctypes.byref(ns),
+               ctypes.byref(tps), ctypes.byref(wgs), ctypes.byref(ws))
     _lib.check(st)
     schedule = "balanced" if sch.value == _lib.MX_SCHEDULE_BALANCED else "split_grid"
     # Launches of a phase-0 call: the balanced schedule and the split grid with one split are
     # one launch; the split grid merges in-kernel up to FUSED_MAX_SPLITS splits when its units'
     # arrival counters fit, else a combine kernel follows (csrc/paged_decode.hip,
-    # kFusedMaxSplits and kMaxSlots).
-    G = num_heads // num_kv_heads
-    rows = seqlen_q * G
-    per_group = 32 if rows > 16 and head_dim <= 128 else 16
-    units = batch * num_kv_heads * -(-rows // per_group)
+    # kFusedMaxSplits and kMaxSlots).  The split grid launches units x splits workgroups.
+    units = wgs.value // max(ns.value, 1)
     two = (schedule == "split_grid" and ns.value > 1 and
            (ns.value > FUSED_MAX_SPLITS or units > COUNTER_SLOTS))
     return {"schedule": schedule, "splits": ns.value, "tokens_per_split": tps.value,
@@ -247,24 +244,28 @@ class BoundDecode:
 
     def __init__(self, q, k_cache, v_cache, block_table, seq_lens, scale=None, *, out=None,
                  causal: bool = False, num_splits: int = 0, max_seq_len: int = 0,
-                 workspace=None, stream=None):
+                 workspace=None, stream=None, k_scale: float = 1.0, v_scale: float = 1.0):
         # validate once through the tensor-level entry (phase 0 runs a real call)
         self.out = paged_gqa_decode(q, k_cache, v_cache, block_table, seq_lens, scale, out=out,
                                     causal=causal, num_splits=num_splits,
-                                    max_seq_len=max_seq_len, workspace=workspace, stream=stream)
+                                    max_seq_len=max_seq_len, workspace=workspace, stream=stream,
+                                    k_scale=k_scale, v_scale=v_scale)
         B, SQ, Hq, D = _query_shape(q)
         num_pages, P, Hkv, _ = k_cache.shape
         if scale is None:
             scale = 1.0 / math.sqrt(D)
+        fp8 = k_cache.dtype == torch.float8_e4m3fn
         self.plan = plan(B, Hq, Hkv, D, P, block_table.shape[1], max_seq_len, num_splits,
-                         seqlen_q=SQ)
+                         seqlen_q=SQ, fp8=fp8)
         self._keep = (q, k_cache, v_cache, block_table, seq_lens, workspace)
         ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-        self._fn = _lib.load().mx_paged_gqa_decode
+        lib = _lib.load()
+        self._fn = lib.mx_paged_gqa_decode_fp8kv if fp8 else lib.mx_paged_gqa_decode
+        scales = [float(k_scale), float(v_scale)] if fp8 else []
         self._args = [_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(self.out), _ptr(seq_lens),
                       _ptr(block_table), B, SQ, Hq, Hkv, D, P, num_pages, block_table.shape[1],
-                      max_seq_len, int(bool(causal)), float(scale), num_splits, _ptr(workspace),
-                      ws_bytes]
+                      max_seq_len, int(bool(causal)), float(scale), *scales, num_splits,
+                      _ptr(workspace), ws_bytes]
         self._stream = _stream_handle(stream, q.device)
 
     @property

@@ -138,3 +138,38 @@ def test_fp8_random(seed):
                                      causal=causal)
     assert_close_to_oracle(out, ref, label)
     assert read_device_status() == 0, label
+
+
+@pytest.mark.parametrize("ns", [0, 1, 4, 20, -3])
+@pytest.mark.parametrize("Hkv,G,sq,causal", [(2, 1, 1, False), (2, 16, 1, False), (6, 4, 4, True),
+                                             (8, 8, 2, True), (4, 2, 8, True), (4, 3, 5, True)])
+def test_fp8_head_dim_64_paired_heads(Hkv, G, sq, causal, ns):
+    """head_dim 64 with an even number of KV heads and at most 16 query rows per head runs as
+    pairs of adjacent heads read as one head of dim 128 (each query row scores against its own
+    head's keys and keeps its own half of the output); the oracle decodes every head alone.
+    (4, 3, 5) has 15 rows per head; the rest cover one to four 16-row tiles per pair."""
+    lens = [0, 1, 17, 250, 1111, 2048]
+    q, k8, v8, table, lt = _case(lens, G * Hkv, Hkv, 64, 16, sq=sq, seed=Hkv * 100 + G * sq)
+    label = f"fp8 paired D=64 Hkv={Hkv} G={G} sq={sq} causal={causal} ns={ns}"
+    print(label, flush=True)
+    out = _run(q, k8, v8, table, lt, causal=causal, ns=ns, k_scale=0.6, v_scale=1.7)
+    ref = paged_decode_fp8_reference(q, k8, v8, table, lt, k_scale=0.6, v_scale=1.7,
+                                     causal=causal)
+    assert_close_to_oracle(out, ref, label)
+    assert read_device_status() == 0, label
+
+
+def test_fp8_bound_decode_matches_the_direct_call():
+    """BoundDecode binds the fp8 entry (with its scales) for an fp8 cache."""
+    from mx_flash_attn_kernel_opt__amd import BoundDecode
+    lens = [33, 700, 2049]
+    for D, Hq, Hkv in ((64, 32, 4), (128, 32, 8)):
+        q, k8, v8, table, lt = (t.to(DEV) for t in _case(lens, Hq, Hkv, D, 16, seed=D))
+        a = paged_gqa_decode(q, k8, v8, table, lt, k_scale=0.5, v_scale=2.0)
+        call = BoundDecode(q, k8, v8, table, lt, k_scale=0.5, v_scale=2.0)
+        b = call().clone()
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), f"D={D}"
+        ref = paged_decode_fp8_reference(q.cpu(), k8.cpu(), v8.cpu(), table.cpu(), lt.cpu(),
+                                         k_scale=0.5, v_scale=2.0)
+        assert_close_to_oracle(b.cpu(), ref, f"bound fp8 D={D}")

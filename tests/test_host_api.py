@@ -320,6 +320,29 @@ def test_python_launch_count_mirrors_the_library_constants():
     assert plan(64, 32, 8, 128, 16, 64, 0, 0, num_cus=256)["launches"] == 1   # balanced
 
 
+@pytest.mark.parametrize("B,SQ,Hq,Hkv,ns,paired", [
+    (2, 1, 32, 4, 5, True),      # G = 8: pairs of heads, one 16-row tile
+    (2, 2, 32, 4, 5, True),      # 16 rows per head: still paired
+    (2, 3, 32, 4, 5, False),     # 24 rows per head: two passes per pair would re-read it
+    (2, 1, 12, 3, 5, False),     # odd Hkv
+    (2, 1, 64, 2, 20, True),     # G = 32 > 16 rows: not paired
+])
+def test_fp8_plan_pairs_head_dim_64_heads(B, SQ, Hq, Hkv, ns, paired):
+    """At head_dim 64 the fp8 entry runs adjacent KV heads in pairs (one unit of work per pair)
+    when a head's query rows fit one 16-row tile; the workspace size covers both formats."""
+    if Hq // Hkv * SQ > 16:
+        paired = False
+    a = plan(B, Hq, Hkv, 64, 16, 64, 0, ns, num_cus=256, seqlen_q=SQ)
+    b = plan(B, Hq, Hkv, 64, 16, 64, 0, ns, num_cus=256, seqlen_q=SQ, fp8=True)
+    assert b["splits"] == a["splits"] > 1
+    assert b["workgroups"] * (2 if paired else 1) == a["workgroups"]
+    n = _lib.load().mx_paged_gqa_decode_workspace_size(B, SQ, Hq, Hkv, 64, 16, 64, 0, ns)
+    assert n >= max(a["workspace_bytes"], b["workspace_bytes"])
+    for D in (128, 256):   # other head dims: the same plan for both formats
+        assert (plan(B, Hq, Hkv, D, 16, 64, 0, ns, num_cus=256, seqlen_q=SQ) ==
+                plan(B, Hq, Hkv, D, 16, 64, 0, ns, num_cus=256, seqlen_q=SQ, fp8=True))
+
+
 # ------------------------------------------------------------------------------------------
 # Sharded-decode entry points: validation (no HIP call is reached on these paths)
 # ------------------------------------------------------------------------------------------
