@@ -673,6 +673,16 @@ def main(argv=None) -> int:
             if child.returncode != 0 or not lines:
                 raise RuntimeError(f"bench of {name} failed:\n{child.stderr[-2000:]}")
             print(lines[-1], flush=True)
+        # The fp8 (e4m3fn) cache on the headline shape and at head_dim 64 (paired heads).
+        for name in (W.BENCH_DEFAULT, "sweep_d64"):
+            cmd = [sys.executable, os.path.abspath(__file__), "--workload", name, "--kv-dtype",
+                   "fp8", "--steps", str(args.steps), "--warmup", str(args.warmup), "--seed",
+                   str(args.seed), "--no-cpu-baseline"] + (["--graph"] if args.graph else [])
+            child = subprocess.run(cmd, capture_output=True, text=True)
+            lines = [ln for ln in child.stdout.splitlines() if ln.startswith("{")]
+            if child.returncode != 0 or not lines:
+                raise RuntimeError(f"fp8 bench of {name} failed:\n{child.stderr[-2000:]}")
+            print(lines[-1], flush=True)
         print(json.dumps(time_append(W.get_spec(W.BENCH_DEFAULT), 200, 20, args.seed)),
               flush=True)
         for name in ("tiny", W.BENCH_DEFAULT):
