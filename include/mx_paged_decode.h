@@ -275,6 +275,37 @@ int mx_paged_gqa_decode_append(const void* q, const void* k_new, const void* v_n
                                float scale, int64_t num_splits, void* workspace,
                                int64_t workspace_bytes, void* stream);
 
+/*
+ * The paged append into an fp8 (e4m3fn) cache: as mx_paged_kv_append, with k_new / v_new bf16
+ * and k_cache / v_cache holding one e4m3fn byte per element.  Each value x is stored as the
+ * e4m3fn value nearest to x / k_scale (x / v_scale for V; the correctly rounded fp32 quotient,
+ * ties to even), the quotient saturated to [-448, 448] first; NaN stays NaN.  k_scale and
+ * v_scale must be finite and > 0.  These are the scales the fp8 decode multiplies back.
+ * No counterpart in the reference (bf16 caches only).
+ */
+int mx_paged_kv_append_fp8kv(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                             const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
+                             int64_t seqlen_new, int64_t num_kv_heads, int64_t head_dim,
+                             int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
+                             float k_scale, float v_scale, void* workspace, void* stream);
+
+/*
+ * Append-and-attend on an fp8 cache: mx_paged_kv_append_fp8kv, then mx_paged_gqa_decode_fp8kv
+ * over seq_lens[b] + seqlen_new keys, with mx_paged_gqa_decode_append's arguments plus the two
+ * scales.  Two launches whatever seqlen_new (the one-launch path writes bf16 rows).
+ * No counterpart in the reference (bf16 caches only).
+ */
+int mx_paged_gqa_decode_append_fp8kv(const void* q, const void* k_new, const void* v_new,
+                                     void* k_cache, void* v_cache, void* out,
+                                     const int32_t* seq_lens, const int32_t* block_table,
+                                     int64_t batch, int64_t seqlen_q, int64_t seqlen_new,
+                                     int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                                     int64_t page_size, int64_t num_pages,
+                                     int64_t max_pages_per_seq, int64_t max_seq_len,
+                                     int32_t causal, float scale, float k_scale, float v_scale,
+                                     int64_t num_splits, void* workspace, int64_t workspace_bytes,
+                                     void* stream);
+
 /* Copies the sticky device status word (MX_DEVICE_* bits) of a workspace (NULL = the library's
  * workspace of the current device) to *flags_out after synchronising the stream; clears it
  * when reset != 0.  Not part of the reference (which validates nothing on the device). */

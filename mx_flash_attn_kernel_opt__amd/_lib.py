@@ -72,6 +72,11 @@ SIGNATURES = {
         ctypes.c_int,
         [_VP] * 8 + [_I64] * 10 + [_I32, _F32, _I64, _VP, _I64, _VP],
     ),
+    "mx_paged_kv_append_fp8kv": (ctypes.c_int, [_VP] * 6 + [_I64] * 7 + [_F32, _F32, _VP, _VP]),
+    "mx_paged_gqa_decode_append_fp8kv": (
+        ctypes.c_int,
+        [_VP] * 8 + [_I64] * 10 + [_I32, _F32, _F32, _F32, _I64, _VP, _I64, _VP],
+    ),
     "mx_read_device_status": (ctypes.c_int, [_VP, _I32, _VP, _P32]),
     "mx_last_status": (ctypes.c_int, []),
     "mx_last_error": (ctypes.c_char_p, []),

@@ -1871,6 +1871,58 @@ __global__ __launch_bounds__(256) void mx_paged_kv_append_kernel(
   for (int i = lane; i < row_vec16; i += 64) dst[i] = src[i];
 }
 
+// The append into an fp8 (e4m3fn) cache: the same slots, each bf16 value x stored as the OCP
+// e4m3fn value nearest to x / scale (ties to even), with x / scale clamped to [-448, 448]
+// first (saturation; NaN stays NaN).  One wave per (new token, K or V); a lane converts 8
+// values per step, one 16-byte load of bf16 into one 8-byte store of fp8.
+__device__ __forceinline__ float fp8_saturate(float v) {
+  return v > 448.f ? 448.f : (v < -448.f ? -448.f : v);  // comparisons pass NaN through
+}
+
+__device__ __forceinline__ uint32_t bf16x4_to_fp8x4(uint32_t lo, uint32_t hi, float scale) {
+  // x / scale is the correctly rounded fp32 quotient (hipcc's default for fp32 division).
+  const float a = fp8_saturate(__uint_as_float(lo << 16) / scale);
+  const float b = fp8_saturate(__uint_as_float(lo & 0xffff0000u) / scale);
+  const float c = fp8_saturate(__uint_as_float(hi << 16) / scale);
+  const float d = fp8_saturate(__uint_as_float(hi & 0xffff0000u) / scale);
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);  // bytes 0, 1
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);       // bytes 2, 3
+  return (uint32_t)w;
+}
+
+__global__ __launch_bounds__(256) void mx_paged_kv_append_fp8_kernel(
+    const uint16_t* __restrict__ k_new, const uint16_t* __restrict__ v_new,
+    uint8_t* __restrict__ k_cache, uint8_t* __restrict__ v_cache,
+    const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ block_table, int batch,
+    int seqlen_new, int row_vec8, int page_size, int num_pages, int max_pages, float k_scale,
+    float v_scale, uint32_t* __restrict__ status) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
+  if (wave >= 2 * batch * seqlen_new) return;
+  const int tok = wave >> 1;
+  const bool is_v = (wave & 1) != 0;
+  const int b = tok / seqlen_new;
+  const int j = tok - b * seqlen_new;
+  const int pos = max(seq_lens[b], 0) + j;
+  if (pos >= max_pages * page_size) {
+    if (lane == 0 && !is_v) atomicOr(status, (uint32_t)MX_DEVICE_SEQ_TOO_LONG);
+    return;
+  }
+  const int pid = block_table[(int64_t)b * max_pages + pos / page_size];
+  if (pid < 0 || pid >= num_pages) {
+    if (lane == 0 && !is_v) atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
+    return;
+  }
+  const u32x4* src = reinterpret_cast<const u32x4*>(is_v ? v_new : k_new) + (int64_t)tok * row_vec8;
+  u32x2* dst = reinterpret_cast<u32x2*>(is_v ? v_cache : k_cache) +
+               ((int64_t)pid * page_size + pos % page_size) * row_vec8;
+  const float scale = is_v ? v_scale : k_scale;
+  for (int i = lane; i < row_vec8; i += 64) {
+    const u32x4 x = src[i];
+    dst[i] = u32x2{bf16x4_to_fp8x4(x[0], x[1], scale), bf16x4_to_fp8x4(x[2], x[3], scale)};
+  }
+}
+
 // ------------------------------------------------------------------------------------------
 // Host side: errors, planning, workspace, launch
 // ------------------------------------------------------------------------------------------
@@ -2515,14 +2567,24 @@ int launch_append(const void* k_new, const void* v_new, void* k_cache, void* v_c
                   const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
                   int64_t seqlen_new, int64_t num_kv_heads, int64_t head_dim,
                   int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
-                  void* workspace, void* stream) {
+                  void* workspace, void* stream, const KvFormat& kv = KvFormat{}) {
   const int64_t waves = 2 * batch * seqlen_new;
-  hipLaunchKernelGGL(mx_paged_kv_append_kernel, dim3((unsigned)ceil_div(waves, 4)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(k_new),
-                     static_cast<const uint16_t*>(v_new), static_cast<uint16_t*>(k_cache),
-                     static_cast<uint16_t*>(v_cache), seq_lens, block_table, (int)batch,
-                     (int)seqlen_new, (int)(num_kv_heads * head_dim / 8), (int)page_size,
-                     (int)num_pages, (int)max_pages_per_seq, static_cast<uint32_t*>(workspace));
+  if (kv.fp8)
+    hipLaunchKernelGGL(mx_paged_kv_append_fp8_kernel, dim3((unsigned)ceil_div(waves, 4)),
+                       dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(k_new), static_cast<const uint16_t*>(v_new),
+                       static_cast<uint8_t*>(k_cache), static_cast<uint8_t*>(v_cache), seq_lens,
+                       block_table, (int)batch, (int)seqlen_new,
+                       (int)(num_kv_heads * head_dim / 8), (int)page_size, (int)num_pages,
+                       (int)max_pages_per_seq, kv.k_scale, kv.v_scale,
+                       static_cast<uint32_t*>(workspace));
+  else
+    hipLaunchKernelGGL(mx_paged_kv_append_kernel, dim3((unsigned)ceil_div(waves, 4)), dim3(256),
+                       0, static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(k_new),
+                       static_cast<const uint16_t*>(v_new), static_cast<uint16_t*>(k_cache),
+                       static_cast<uint16_t*>(v_cache), seq_lens, block_table, (int)batch,
+                       (int)seqlen_new, (int)(num_kv_heads * head_dim / 8), (int)page_size,
+                       (int)num_pages, (int)max_pages_per_seq, static_cast<uint32_t*>(workspace));
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return fail(MX_STATUS_HIP_ERROR, std::string("kernel launch failed: ") + hipGetErrorString(e));
@@ -2688,11 +2750,12 @@ int mx_read_device_status(void* workspace, int32_t reset, void* stream, int32_t*
   return ok();
 }
 
-int mx_paged_kv_append(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
-                       const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
-                       int64_t seqlen_new, int64_t num_kv_heads, int64_t head_dim,
-                       int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
-                       void* workspace, void* stream) {
+// Shared by mx_paged_kv_append and mx_paged_kv_append_fp8kv.
+static int kv_append_impl(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                          const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
+                          int64_t seqlen_new, int64_t num_kv_heads, int64_t head_dim,
+                          int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
+                          void* workspace, void* stream, const KvFormat& kv) {
   int st = check_append(k_new, v_new, k_cache, v_cache, seq_lens, block_table, batch, seqlen_new,
                         num_kv_heads, head_dim, page_size, num_pages, max_pages_per_seq);
   if (st != MX_STATUS_OK) return st;
@@ -2703,7 +2766,87 @@ int mx_paged_kv_append(const void* k_new, const void* v_new, void* k_cache, void
   }
   return launch_append(k_new, v_new, k_cache, v_cache, seq_lens, block_table, batch, seqlen_new,
                        num_kv_heads, head_dim, page_size, num_pages, max_pages_per_seq,
-                       workspace, stream);
+                       workspace, stream, kv);
+}
+
+// Shared by mx_paged_gqa_decode_append and mx_paged_gqa_decode_append_fp8kv.
+static int decode_append_impl(const void* q, const void* k_new, const void* v_new,
+                              void* k_cache, void* v_cache, void* out, const int32_t* seq_lens,
+                              const int32_t* block_table, int64_t batch, int64_t seqlen_q,
+                              int64_t seqlen_new, int64_t num_heads, int64_t num_kv_heads,
+                              int64_t head_dim, int64_t page_size, int64_t num_pages,
+                              int64_t max_pages_per_seq, int64_t max_seq_len, int32_t causal,
+                              float scale, int64_t num_splits, void* workspace,
+                              int64_t workspace_bytes, void* stream, const KvFormat& kv) {
+  if (!q || !out)
+    return fail(MX_STATUS_NULL_POINTER, "q and out must be non-NULL");
+  int st = check_append(k_new, v_new, k_cache, v_cache, seq_lens, block_table, batch, seqlen_new,
+                        num_kv_heads, head_dim, page_size, num_pages, max_pages_per_seq);
+  if (st != MX_STATUS_OK) return st;
+  if (seqlen_new > INT32_MAX / 2)
+    return fail(MX_STATUS_UNSUPPORTED, "seqlen_new must be < 2^30");
+  Plan plan;
+  const KernelHeads kh = kernel_heads(seqlen_q, num_heads, num_kv_heads, head_dim, kv.fp8);
+  st = prepare_decode(q, k_cache, v_cache, out, batch, seqlen_q, num_heads, kh.kv_heads,
+                      kh.head_dim, page_size, num_pages, max_pages_per_seq, max_seq_len, causal,
+                      scale, num_splits, &workspace, workspace_bytes, 0, &plan);
+  if (st != MX_STATUS_OK) return st;
+  AppendArgs app;
+  const bool lds_k = kh.head_dim == 64    ? k_via_lds<64>()
+                     : kh.head_dim == 128 ? k_via_lds<128>()
+                                          : k_via_lds<256>();
+  if (seqlen_new >= 1 && seqlen_new <= kChunk && lds_k && !kv.fp8) {
+    // One launch: the new keys are one extra chunk of each unit, written to the cache by the
+    // wave that loads them.
+    app.new_tokens = (int)seqlen_new;
+    app.k_new = k_new;
+    app.v_new = v_new;
+  } else if (seqlen_new > 0) {
+    // Longer appends, and every append into an fp8 cache: the append kernel first, then the
+    // decode over seq_lens + seqlen_new.
+    st = launch_append(k_new, v_new, k_cache, v_cache, seq_lens, block_table, batch, seqlen_new,
+                       num_kv_heads, head_dim, page_size, num_pages, max_pages_per_seq,
+                       workspace, stream, kv);
+    if (st != MX_STATUS_OK) return st;
+    app.appended = (int)seqlen_new;
+  }
+  return run_decode(plan, q, k_cache, v_cache, out, nullptr, nullptr, seq_lens, block_table,
+                    batch, seqlen_q, num_heads, kh.kv_heads, kh.head_dim, page_size, num_pages,
+                    max_pages_per_seq, causal, scale, workspace, 0, app, stream, kv,
+                    kh.pair_group);
+}
+
+// Scales of an append into an fp8 cache: the stored values are x / scale.
+static int check_fp8_append_scales(float k_scale, float v_scale) {
+  if (!(std::isfinite(k_scale) && std::isfinite(v_scale) && k_scale > 0.f && v_scale > 0.f))
+    return fail(MX_STATUS_INVALID_ARGUMENT, "k_scale and v_scale must be finite and > 0");
+  return MX_STATUS_OK;
+}
+
+int mx_paged_kv_append(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                       const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
+                       int64_t seqlen_new, int64_t num_kv_heads, int64_t head_dim,
+                       int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
+                       void* workspace, void* stream) {
+  return kv_append_impl(k_new, v_new, k_cache, v_cache, seq_lens, block_table, batch, seqlen_new,
+                        num_kv_heads, head_dim, page_size, num_pages, max_pages_per_seq,
+                        workspace, stream, KvFormat{});
+}
+
+int mx_paged_kv_append_fp8kv(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                             const int32_t* seq_lens, const int32_t* block_table, int64_t batch,
+                             int64_t seqlen_new, int64_t num_kv_heads, int64_t head_dim,
+                             int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
+                             float k_scale, float v_scale, void* workspace, void* stream) {
+  const int st = check_fp8_append_scales(k_scale, v_scale);
+  if (st != MX_STATUS_OK) return st;
+  KvFormat kv;
+  kv.fp8 = true;
+  kv.k_scale = k_scale;
+  kv.v_scale = v_scale;
+  return kv_append_impl(k_new, v_new, k_cache, v_cache, seq_lens, block_table, batch, seqlen_new,
+                        num_kv_heads, head_dim, page_size, num_pages, max_pages_per_seq,
+                        workspace, stream, kv);
 }
 
 int mx_paged_gqa_decode_append(const void* q, const void* k_new, const void* v_new,
@@ -2714,41 +2857,34 @@ int mx_paged_gqa_decode_append(const void* q, const void* k_new, const void* v_n
                                int64_t max_pages_per_seq, int64_t max_seq_len, int32_t causal,
                                float scale, int64_t num_splits, void* workspace,
                                int64_t workspace_bytes, void* stream) {
-  if (!q || !out)
-    return fail(MX_STATUS_NULL_POINTER, "q and out must be non-NULL");
-  int st = check_append(k_new, v_new, k_cache, v_cache, seq_lens, block_table, batch, seqlen_new,
-                        num_kv_heads, head_dim, page_size, num_pages, max_pages_per_seq);
+  return decode_append_impl(q, k_new, v_new, k_cache, v_cache, out, seq_lens, block_table,
+                            batch, seqlen_q, seqlen_new, num_heads, num_kv_heads, head_dim,
+                            page_size, num_pages, max_pages_per_seq, max_seq_len, causal, scale,
+                            num_splits, workspace, workspace_bytes, stream, KvFormat{});
+}
+
+int mx_paged_gqa_decode_append_fp8kv(const void* q, const void* k_new, const void* v_new,
+                                     void* k_cache, void* v_cache, void* out,
+                                     const int32_t* seq_lens, const int32_t* block_table,
+                                     int64_t batch, int64_t seqlen_q, int64_t seqlen_new,
+                                     int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                                     int64_t page_size, int64_t num_pages,
+                                     int64_t max_pages_per_seq, int64_t max_seq_len,
+                                     int32_t causal, float scale, float k_scale, float v_scale,
+                                     int64_t num_splits, void* workspace, int64_t workspace_bytes,
+                                     void* stream) {
+  int st = check_fp8_append_scales(k_scale, v_scale);
   if (st != MX_STATUS_OK) return st;
-  if (seqlen_new > INT32_MAX / 2)
-    return fail(MX_STATUS_UNSUPPORTED, "seqlen_new must be < 2^30");
-  Plan plan;
-  const KernelHeads kh = kernel_heads(seqlen_q, num_heads, num_kv_heads, head_dim, false);
-  st = prepare_decode(q, k_cache, v_cache, out, batch, seqlen_q, num_heads, kh.kv_heads,
-                      kh.head_dim, page_size, num_pages, max_pages_per_seq, max_seq_len, causal,
-                      scale, num_splits, &workspace, workspace_bytes, 0, &plan);
-  if (st != MX_STATUS_OK) return st;
-  AppendArgs app;
-  const bool lds_k = kh.head_dim == 64    ? k_via_lds<64>()
-                     : kh.head_dim == 128 ? k_via_lds<128>()
-                                          : k_via_lds<256>();
-  if (seqlen_new >= 1 && seqlen_new <= kChunk && lds_k) {
-    // One launch: the new keys are one extra chunk of each unit, written to the cache by the
-    // wave that loads them.
-    app.new_tokens = (int)seqlen_new;
-    app.k_new = k_new;
-    app.v_new = v_new;
-  } else if (seqlen_new > 0) {
-    // Longer appends: the append kernel first, then the decode over seq_lens + seqlen_new.
-    st = launch_append(k_new, v_new, k_cache, v_cache, seq_lens, block_table, batch, seqlen_new,
-                       num_kv_heads, head_dim, page_size, num_pages, max_pages_per_seq,
-                       workspace, stream);
-    if (st != MX_STATUS_OK) return st;
-    app.appended = (int)seqlen_new;
-  }
-  return run_decode(plan, q, k_cache, v_cache, out, nullptr, nullptr, seq_lens, block_table,
-                    batch, seqlen_q, num_heads, kh.kv_heads, kh.head_dim, page_size, num_pages,
-                    max_pages_per_seq, causal, scale, workspace, 0, app, stream, KvFormat{},
-                    kh.pair_group);
+  if (!std::isfinite(scale * k_scale))
+    return fail(MX_STATUS_INVALID_ARGUMENT, "scale * k_scale must be finite");
+  KvFormat kv;
+  kv.fp8 = true;
+  kv.k_scale = k_scale;
+  kv.v_scale = v_scale;
+  return decode_append_impl(q, k_new, v_new, k_cache, v_cache, out, seq_lens, block_table,
+                            batch, seqlen_q, seqlen_new, num_heads, num_kv_heads, head_dim,
+                            page_size, num_pages, max_pages_per_seq, max_seq_len, causal, scale,
+                            num_splits, workspace, workspace_bytes, stream, kv);
 }
 
 int mx_last_status(void) { return g_last_status; }

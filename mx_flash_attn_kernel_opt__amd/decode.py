@@ -298,18 +298,25 @@ def run_kernel(q, k_cache_paged, v_cache_paged, output, cache_seqlens, block_tab
 
 def paged_kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
                     v_cache: torch.Tensor, block_table: torch.Tensor, seq_lens: torch.Tensor,
-                    *, workspace: torch.Tensor | None = None, stream=None) -> None:
+                    *, workspace: torch.Tensor | None = None, stream=None,
+                    k_scale: float = 1.0, v_scale: float = 1.0) -> None:
     """Write new tokens' K/V into their page slots (flash_attn_with_kvcache's k / v append).
 
     k_new / v_new: [B, S, Hkv, D] (or [B, Hkv, D] for one token) bf16; token j of sequence b
     goes to position max(seq_lens[b], 0) + j of that sequence's block-table row.  seq_lens are
     the lengths before the append and are not modified.  Slots past the table row or with a
-    page id outside the pool are skipped and flagged (read_device_status).
+    page id outside the pool are skipped and flagged (read_device_status).  Into
+    float8_e4m3fn caches each value x is stored as the e4m3fn value nearest to x / k_scale
+    (x / v_scale for V), saturated to +-448.
     """
     _require(k_new.is_cuda, "k_new must be a device tensor")
     dev = k_new.device
+    fp8 = k_cache.dtype == torch.float8_e4m3fn
+    _require(fp8 or (k_scale == 1.0 and v_scale == 1.0),
+             "k_scale / v_scale apply to float8_e4m3fn caches only")
+    kv_dt = torch.float8_e4m3fn if fp8 else torch.bfloat16
     for name, t, dt in (("k_new", k_new, torch.bfloat16), ("v_new", v_new, torch.bfloat16),
-                        ("k_cache", k_cache, torch.bfloat16), ("v_cache", v_cache, torch.bfloat16),
+                        ("k_cache", k_cache, kv_dt), ("v_cache", v_cache, kv_dt),
                         ("block_table", block_table, torch.int32),
                         ("seq_lens", seq_lens, torch.int32)):
         _require(t.device == dev, f"{name} must be on {dev}")
@@ -332,11 +339,15 @@ def paged_kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Ten
     ws = None if workspace is None else workspace
     if ws is not None:
         _require(ws.is_cuda and ws.device == dev, "workspace must be on the same device")
+    lib = _lib.load()
+    common = [_ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache), _ptr(seq_lens),
+              _ptr(block_table), B, S, Hkv, D, P, num_pages, block_table.shape[1]]
     with torch.cuda.device(dev):
-        st = _lib.load().mx_paged_kv_append(
-            _ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache), _ptr(seq_lens),
-            _ptr(block_table), B, S, Hkv, D, P, num_pages, block_table.shape[1], _ptr(ws),
-            _stream_handle(stream, dev))
+        if fp8:
+            st = lib.mx_paged_kv_append_fp8kv(*common, float(k_scale), float(v_scale), _ptr(ws),
+                                              _stream_handle(stream, dev))
+        else:
+            st = lib.mx_paged_kv_append(*common, _ptr(ws), _stream_handle(stream, dev))
     _lib.check(st)
 
 
@@ -346,7 +357,8 @@ def paged_gqa_decode_append(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.T
                             scale: float | None = None, *, out: torch.Tensor | None = None,
                             causal: bool = False, num_splits: int = 0, max_seq_len: int = 0,
                             workspace: torch.Tensor | None = None,
-                            stream=None) -> torch.Tensor:
+                            stream=None, k_scale: float = 1.0,
+                            v_scale: float = 1.0) -> torch.Tensor:
     """Append the new tokens' K/V to the paged cache, then decode over the cache including them
     (flash_attn_with_kvcache with k / v given).
 
@@ -356,23 +368,32 @@ def paged_gqa_decode_append(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.T
     token i sees keys t < L + S - seqlen_q + i + 1.  Returns the bf16 output shaped like q.
     For S <= 16 the append and the attention are one kernel launch (the new keys are read from
     k_new / v_new as one more chunk and written to the cache by the same kernel); longer
-    appends run the append kernel first.
+    appends run the append kernel first.  float8_e4m3fn caches take per-tensor scales (see
+    paged_kv_append and paged_gqa_decode) and always run the append kernel first.
     """
-    args, out = _append_call_args(q, k_new, v_new, k_cache, v_cache, block_table, seq_lens,
-                                  scale, out, causal, num_splits, max_seq_len, workspace)
+    args, out, fp8 = _append_call_args(q, k_new, v_new, k_cache, v_cache, block_table,
+                                       seq_lens, scale, out, causal, num_splits, max_seq_len,
+                                       workspace, k_scale, v_scale)
     dev = q.device
+    lib = _lib.load()
+    fn = lib.mx_paged_gqa_decode_append_fp8kv if fp8 else lib.mx_paged_gqa_decode_append
     with torch.cuda.device(dev):
-        st = _lib.load().mx_paged_gqa_decode_append(*args, _stream_handle(stream, dev))
+        st = fn(*args, _stream_handle(stream, dev))
     _lib.check(st)
     return out
 
 
 def _append_call_args(q, k_new, v_new, k_cache, v_cache, block_table, seq_lens, scale, out,
-                      causal, num_splits, max_seq_len, workspace):
+                      causal, num_splits, max_seq_len, workspace, k_scale=1.0, v_scale=1.0):
     """Python-side checks of an append-and-attend call and its C arguments (all but the
-    stream), with the output tensor (allocated when ``out`` is None)."""
+    stream), with the output tensor (allocated when ``out`` is None) and whether the caches
+    are fp8 (the arguments are then those of the _fp8kv entry)."""
     dev, B, SQ, Hq, D, num_pages, P, Hkv = _check_decode_inputs(q, k_cache, v_cache,
-                                                                block_table, seq_lens)
+                                                                block_table, seq_lens,
+                                                                allow_fp8=True)
+    fp8 = k_cache.dtype == torch.float8_e4m3fn
+    _require(fp8 or (k_scale == 1.0 and v_scale == 1.0),
+             "k_scale / v_scale apply to float8_e4m3fn caches only")
     _require(k_new.shape == v_new.shape, "k_new and v_new must have the same shape")
     for name, t in (("k_new", k_new), ("v_new", v_new)):
         _require(t.device == dev and t.dtype == torch.bfloat16 and t.is_contiguous(),
@@ -392,11 +413,12 @@ def _append_call_args(q, k_new, v_new, k_cache, v_cache, block_table, seq_lens, 
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     ws_bytes = _workspace_bytes(workspace, dev)
+    scales = [float(k_scale), float(v_scale)] if fp8 else []
     args = [_ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache), _ptr(out),
             _ptr(seq_lens), _ptr(block_table), B, SQ, S, Hq, Hkv, D, P, num_pages,
-            block_table.shape[1], max_seq_len, int(bool(causal)), float(scale), num_splits,
-            _ptr(workspace), ws_bytes]
-    return args, out
+            block_table.shape[1], max_seq_len, int(bool(causal)), float(scale), *scales,
+            num_splits, _ptr(workspace), ws_bytes]
+    return args, out, fp8
 
 
 class BoundDecodeAppend:
@@ -412,12 +434,15 @@ class BoundDecodeAppend:
 
     def __init__(self, q, k_new, v_new, k_cache, v_cache, block_table, seq_lens, scale=None, *,
                  out=None, causal: bool = False, num_splits: int = 0, max_seq_len: int = 0,
-                 workspace=None, stream=None):
-        self._args, self.out = _append_call_args(q, k_new, v_new, k_cache, v_cache,
-                                                 block_table, seq_lens, scale, out, causal,
-                                                 num_splits, max_seq_len, workspace)
+                 workspace=None, stream=None, k_scale: float = 1.0, v_scale: float = 1.0):
+        self._args, self.out, fp8 = _append_call_args(q, k_new, v_new, k_cache, v_cache,
+                                                      block_table, seq_lens, scale, out, causal,
+                                                      num_splits, max_seq_len, workspace,
+                                                      k_scale, v_scale)
         self._keep = (q, k_new, v_new, k_cache, v_cache, block_table, seq_lens, workspace)
-        self._fn = _lib.load().mx_paged_gqa_decode_append
+        lib = _lib.load()
+        self._fn = (lib.mx_paged_gqa_decode_append_fp8kv if fp8
+                    else lib.mx_paged_gqa_decode_append)
         self._stream = _stream_handle(stream, q.device)
 
     def __call__(self) -> torch.Tensor:

@@ -37,6 +37,11 @@ Pinning (what each function is checked against, in tests/test_oracle.py):
                           caches dequantized by torch's e4m3fn conversion; pinned by known
                           e4m3fn codes (1, 448, the smallest subnormal, -0, NaN), by agreement
                           with the bf16 oracle on the same values and by scale linearity.
+  fp8_quantize            what an append into an fp8 cache stores (x / scale saturated to
+                          +-448, rounded to nearest even by torch's conversion); pinned by
+                          closed-form codes (ties to even at normal and subnormal steps,
+                          saturation, signed zero, NaN), by the round trip of all 256 codes
+                          and by the half-step error bound.
 No reference-held fixtures exist for this path (the reference checks live against the absent
 third-party flash_attn_with_kvcache, verify_real.py:40-41), so parity with that library is
 unpinned; the task.md:85-96 example is kept as a shape fixture under tests/golden/.
@@ -45,6 +50,7 @@ unpinned; the task.md:85-96 example is kept as a shape fixture under tests/golde
 from .paged_attention import (  # noqa: F401
     combine_partials,
     fp8_dequantize,
+    fp8_quantize,
     kv_bytes,
     lse_merge_reference,
     paged_decode_append_reference,

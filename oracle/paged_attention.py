@@ -93,6 +93,16 @@ def fp8_dequantize(cache: torch.Tensor, scale: float) -> torch.Tensor:
     return cache.float() * float(scale)
 
 
+def fp8_quantize(x: torch.Tensor, scale: float) -> torch.Tensor:
+    """float8_e4m3fn values of x / scale (fp32 quotient), saturated to [-448, 448] (NaN stays
+    NaN) and rounded to nearest, ties to even (torch's conversion): what an append into a
+    per-tensor-scaled fp8 cache stores."""
+    v = x.float() / torch.tensor(float(scale), dtype=torch.float32)
+    v = torch.where(v > 448.0, torch.full_like(v, 448.0),
+                    torch.where(v < -448.0, torch.full_like(v, -448.0), v))
+    return v.to(torch.float8_e4m3fn)
+
+
 def paged_decode_fp8_reference(q, k_cache, v_cache, block_table, seq_lens, scale=None,
                                k_scale: float = 1.0, v_scale: float = 1.0,
                                causal: bool = False) -> torch.Tensor:
@@ -201,16 +211,21 @@ def combine_partials(o: np.ndarray, lse: np.ndarray, nsv) -> np.ndarray:
     return out
 
 
-def paged_kv_append_reference(k_new, v_new, k_cache, v_cache, block_table, seq_lens):
+def paged_kv_append_reference(k_new, v_new, k_cache, v_cache, block_table, seq_lens,
+                              k_scale: float = 1.0, v_scale: float = 1.0):
     """Paged K/V append on CPU copies (flash_attn_with_kvcache's k / v arguments; the reference's
     harness passes them as None, verify_real.py:40-41): token j of sequence b is stored at
     position pos = max(L_b, 0) + j, page block_table[b, pos // P], offset pos % P
     (task.md:94, 146).  Slots past the table row or with a page id outside the pool are
-    skipped.  Returns (k_cache, v_cache, flags) with flags a set of {"seq_too_long",
-    "bad_page"}."""
+    skipped.  float8_e4m3fn caches store fp8_quantize(x, k_scale) / (x, v_scale).  Returns
+    (k_cache, v_cache, flags) with flags a set of {"seq_too_long", "bad_page"}."""
     k_out, v_out = k_cache.clone(), v_cache.clone()
     kn = k_new if k_new.dim() == 4 else k_new.unsqueeze(1)
     vn = v_new if v_new.dim() == 4 else v_new.unsqueeze(1)
+    if k_cache.dtype == torch.float8_e4m3fn:  # bytes in, bytes out
+        kn, vn = fp8_quantize(kn, k_scale).view(torch.uint8), fp8_quantize(vn, v_scale).view(
+            torch.uint8)
+        k_out, v_out = k_out.view(torch.uint8), v_out.view(torch.uint8)
     B, S = kn.shape[0], kn.shape[1]
     num_pages, P = k_cache.shape[0], k_cache.shape[1]
     width = block_table.shape[1]
@@ -228,6 +243,8 @@ def paged_kv_append_reference(k_new, v_new, k_cache, v_cache, block_table, seq_l
                 continue
             k_out[pid, pos % P] = kn[b, j]
             v_out[pid, pos % P] = vn[b, j]
+    if k_cache.dtype == torch.float8_e4m3fn:
+        k_out, v_out = k_out.view(torch.float8_e4m3fn), v_out.view(torch.float8_e4m3fn)
     return k_out, v_out, flags
 
 

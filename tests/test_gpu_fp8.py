@@ -173,3 +173,113 @@ def test_fp8_bound_decode_matches_the_direct_call():
         ref = paged_decode_fp8_reference(q.cpu(), k8.cpu(), v8.cpu(), table.cpu(), lt.cpu(),
                                          k_scale=0.5, v_scale=2.0)
         assert_close_to_oracle(b.cpu(), ref, f"bound fp8 D={D}")
+
+
+# ------------------------------------------------------------------------------------------
+# Appends into an fp8 cache (quantize on write)
+# ------------------------------------------------------------------------------------------
+
+def _append_case(B, S, Hkv, D, P, width, seed, specials=True):
+    g = torch.Generator().manual_seed(seed)
+    pool = B * width + 2
+    k8 = (torch.randn(pool, P, Hkv, D, generator=g) * 2).to(torch.float8_e4m3fn)
+    v8 = (torch.randn(pool, P, Hkv, D, generator=g)).to(torch.float8_e4m3fn)
+    kn = torch.randn(B, S, Hkv, D, generator=g) * torch.tensor([0.01, 1.0, 30.0, 900.0])[
+        torch.randint(0, 4, (B, S, Hkv, D), generator=g)]
+    vn = torch.randn(B, S, Hkv, D, generator=g) * 3
+    if specials:  # saturation, NaN, infinities, signed zero, subnormal steps and their ties
+        sp = torch.tensor([float("nan"), float("inf"), -float("inf"), -0.0, 0.0, 2.0 ** -10,
+                           3 * 2.0 ** -10, 1.0625, 1.1875, 464.0, -5000.0, 2.0 ** -9])
+        flat = kn.view(-1)
+        idx = torch.randint(0, flat.numel(), (64,), generator=g)
+        flat[idx] = sp[torch.arange(64) % sp.numel()]
+    table = torch.randperm(pool, generator=g)[: B * width].to(torch.int32).view(B, width)
+    lens = torch.randint(0, width * P - S + 1, (B,), generator=g).to(torch.int32)
+    return kn.to(torch.bfloat16), vn.to(torch.bfloat16), k8, v8, table, lens
+
+
+@pytest.mark.parametrize("B,S,Hkv,D,P", [(3, 1, 8, 128, 16), (2, 5, 4, 64, 32), (4, 17, 2, 256, 16),
+                                         (1, 3, 1, 8, 16), (2, 40, 3, 64, 64)])
+@pytest.mark.parametrize("scales", [(1.0, 1.0), (0.37, 2.5)])
+def test_fp8_append_is_bit_exact(B, S, Hkv, D, P, scales):
+    """Each stored byte equals the oracle's quantization: x / scale (correctly rounded fp32),
+    saturated to +-448, nearest e4m3fn with ties to even; NaN stays NaN."""
+    from mx_flash_attn_kernel_opt__amd import paged_kv_append
+    from oracle import paged_kv_append_reference
+    ks, vs = scales
+    kn, vn, k8, v8, table, lens = _append_case(B, S, Hkv, D, P, 4, seed=B * 100 + S + D)
+    label = f"fp8 append B={B} S={S} Hkv={Hkv} D={D} P={P} scales={scales}"
+    print(label, flush=True)
+    kd, vd = k8.to(DEV), v8.to(DEV)
+    paged_kv_append(kn.to(DEV), vn.to(DEV), kd, vd, table.to(DEV), lens.to(DEV),
+                    k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    kr, vr, flags = paged_kv_append_reference(kn, vn, k8, v8, table, lens, k_scale=ks,
+                                              v_scale=vs)
+    assert not flags
+    got_k, got_v = kd.cpu().view(torch.uint8), vd.cpu().view(torch.uint8)
+    want_k, want_v = kr.view(torch.uint8), vr.view(torch.uint8)
+    nan_k = (want_k & 0x7F) == 0x7F
+    assert torch.equal(got_k[~nan_k], want_k[~nan_k]), label
+    assert ((got_k[nan_k] & 0x7F) == 0x7F).all(), label  # NaN of either sign
+    assert torch.equal(got_v, want_v), label
+    assert read_device_status() == 0
+
+
+def test_fp8_append_flags_and_skips_bad_slots():
+    from mx_flash_attn_kernel_opt__amd import _lib, paged_kv_append
+    from oracle import paged_kv_append_reference
+    kn, vn, k8, v8, table, lens = _append_case(3, 4, 2, 64, 16, 2, seed=3, specials=False)
+    table[1, 1] = 10_000           # out of the pool
+    lens[:] = torch.tensor([0, 14, 30], dtype=torch.int32)   # sequence 2 runs past its row
+    kd, vd = k8.to(DEV), v8.to(DEV)
+    paged_kv_append(kn.to(DEV), vn.to(DEV), kd, vd, table.to(DEV), lens.to(DEV), k_scale=0.5,
+                    v_scale=2.0)
+    flags = read_device_status()
+    kr, vr, rflags = paged_kv_append_reference(kn, vn, k8, v8, table, lens, k_scale=0.5,
+                                               v_scale=2.0)
+    assert rflags == {"bad_page", "seq_too_long"}
+    assert flags == _lib.MX_DEVICE_BAD_PAGE_ID | _lib.MX_DEVICE_SEQ_TOO_LONG
+    assert torch.equal(kd.cpu().view(torch.uint8), kr.view(torch.uint8))
+    assert torch.equal(vd.cpu().view(torch.uint8), vr.view(torch.uint8))
+
+
+@pytest.mark.parametrize("S,SQ,causal,ns", [(1, 1, False, 0), (3, 3, True, 0), (1, 1, False, 5),
+                                            (20, 4, True, -3)])
+@pytest.mark.parametrize("D,Hq,Hkv", [(128, 32, 8), (64, 16, 2)])
+def test_fp8_decode_append_matches_the_oracle(S, SQ, causal, ns, D, Hq, Hkv):
+    """Append-and-attend on an fp8 cache: the quantized append, then the fp8 decode over
+    L + S keys; the caches bit-exact, the output within the tolerance; the bound call equal."""
+    from mx_flash_attn_kernel_opt__amd import BoundDecodeAppend, paged_gqa_decode_append
+    from oracle import paged_kv_append_reference
+    B, P = 3, 16
+    kn, vn, k8, v8, table, lens = _append_case(B, S, Hkv, D, P, 40, seed=S * 7 + D,
+                                               specials=False)
+    g = torch.Generator().manual_seed(S + SQ)
+    shape = (B, Hq, D) if SQ == 1 else (B, SQ, Hq, D)
+    q = (torch.randn(*shape, generator=g) * 0.5).to(torch.bfloat16)
+    # V near unit size keeps the bf16 output in the range the tolerance assumes (bf16 rounds
+    # outputs of 8-16 by up to 0.03).
+    kn, vn = kn.float().clamp(-40, 40).to(torch.bfloat16), (vn.float() * 0.25).to(torch.bfloat16)
+    ks, vs = 0.4, 0.8
+    label = f"fp8 decode+append D={D} S={S} SQ={SQ} causal={causal} ns={ns}"
+    print(label, flush=True)
+    kd, vd = k8.to(DEV), v8.to(DEV)
+    out = paged_gqa_decode_append(q.to(DEV), kn.to(DEV), vn.to(DEV), kd, vd, table.to(DEV),
+                                  lens.to(DEV), causal=causal, num_splits=ns, k_scale=ks,
+                                  v_scale=vs)
+    torch.cuda.synchronize()
+    kr, vr, _ = paged_kv_append_reference(kn, vn, k8, v8, table, lens, k_scale=ks, v_scale=vs)
+    assert torch.equal(kd.cpu().view(torch.uint8), kr.view(torch.uint8)), label
+    ref = paged_decode_fp8_reference(q, kr, vr, table, lens + S, k_scale=ks, v_scale=vs,
+                                     causal=causal)
+    assert_close_to_oracle(out.cpu(), ref, label)
+    # The bound call on fresh copies of the caches gives the same bytes and output.
+    kd2, vd2 = k8.to(DEV), v8.to(DEV)
+    step = BoundDecodeAppend(q.to(DEV), kn.to(DEV), vn.to(DEV), kd2, vd2, table.to(DEV),
+                             lens.to(DEV), causal=causal, num_splits=ns, k_scale=ks, v_scale=vs)
+    out2 = step().clone()
+    torch.cuda.synchronize()
+    assert torch.equal(out2.cpu(), out.cpu()), label
+    assert torch.equal(kd2.cpu().view(torch.uint8), kr.view(torch.uint8)), label
+    assert read_device_status() == 0

@@ -646,3 +646,40 @@ def test_fp8_oracle_scales_are_not_swapped():
     assert not torch.allclose(a, swapped, atol=1e-3)
     unit = paged_decode_fp8_reference(q, k8, v8, table, lens, k_scale=2.0, v_scale=1.0)
     assert torch.allclose(a, unit * 0.5, atol=1e-6, rtol=1e-6)
+
+
+def test_fp8_quantize_closed_form_codes():
+    """fp8_quantize against codes the OCP e4m3fn format fixes by hand: 1 = 0x38, 448 = 0x7e
+    (largest finite), saturation above it, 2^-9 = 0x01; ties go to the even code: 2^-10 -> 0,
+    3 * 2^-10 -> 0x02, 1 + 1/16 -> 0x38 (1), 1 + 3/16 -> 0x3a (1.25); -0 keeps its sign; a
+    scale divides first."""
+    from oracle import fp8_quantize
+    vals = [1.0, 448.0, 1000.0, -1000.0, 2.0 ** -9, 2.0 ** -10, 3 * 2.0 ** -10, 0.0, -0.0,
+            1.0625, 1.1875, 464.0, -2.0 ** -9, 0.875]
+    want = [0x38, 0x7E, 0x7E, 0xFE, 0x01, 0x00, 0x02, 0x00, 0x80, 0x38, 0x3A, 0x7E, 0x81, 0x36]
+    x = torch.tensor(vals, dtype=torch.bfloat16)
+    got = fp8_quantize(x, 1.0).view(torch.uint8).tolist()
+    assert got == want, [hex(g) for g in got]
+    assert fp8_quantize(torch.tensor([2.0, -896.0], dtype=torch.bfloat16), 2.0).view(
+        torch.uint8).tolist() == [0x38, 0xFE]
+    nan = fp8_quantize(torch.tensor([float("nan")], dtype=torch.bfloat16), 1.0).view(torch.uint8)
+    assert int(nan[0]) & 0x7F == 0x7F
+    inf = fp8_quantize(torch.tensor([float("inf"), -float("inf")], dtype=torch.bfloat16), 3.0)
+    assert inf.view(torch.uint8).tolist() == [0x7E, 0xFE]
+
+
+def test_fp8_quantize_round_trips_every_code_and_bounds_the_error():
+    from oracle import fp8_dequantize, fp8_quantize
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    finite = [c for c in range(256) if (c & 0x7F) != 0x7F]
+    vals = fp8_dequantize(codes.view(torch.float8_e4m3fn), 1.0)[finite]
+    back = fp8_quantize(vals.to(torch.bfloat16), 1.0).view(torch.uint8)
+    assert back.tolist() == finite
+    # Rounding error of a normal value is at most half a step: |q - x| <= 2^-4 |x|.
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(4096, generator=g) * 20).to(torch.bfloat16)
+    xf = x.float()
+    q = fp8_dequantize(fp8_quantize(x, 1.0), 1.0)
+    normal = xf.abs() >= 2.0 ** -6
+    assert ((q - xf).abs()[normal] <= xf.abs()[normal] * 2.0 ** -4 + 1e-12).all()
+    assert ((q - xf).abs()[~normal] <= 2.0 ** -10 + 1e-12).all()
