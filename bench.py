@@ -191,7 +191,8 @@ def time_graph(inp: W.DecodeInputs, pools, out, ws, num_splits: int, steps: int)
     end.record(cur)
     torch.cuda.synchronize()
     us = start.elapsed_time(end) * 1e3 / (replays * per_graph)
-    return {"us_per_call": round(us, 2), "GBps": round(inp.kv_bytes() / us / 1e3, 1),
+    nbytes = inp.kv_bytes() // (2 if inp.k_cache.dtype == torch.float8_e4m3fn else 1)
+    return {"us_per_call": round(us, 2), "GBps": round(nbytes / us / 1e3, 1),
             "calls_per_graph": per_graph, "replays": replays}
 
 
