@@ -290,9 +290,11 @@ int mx_paged_kv_append_fp8kv(const void* k_new, const void* v_new, void* k_cache
                              float k_scale, float v_scale, void* workspace, void* stream);
 
 /*
- * Append-and-attend on an fp8 cache: mx_paged_kv_append_fp8kv, then mx_paged_gqa_decode_fp8kv
- * over seq_lens[b] + seqlen_new keys, with mx_paged_gqa_decode_append's arguments plus the two
- * scales.  Two launches whatever seqlen_new (the one-launch path writes bf16 rows).
+ * Append-and-attend on an fp8 cache: what mx_paged_kv_append_fp8kv and then
+ * mx_paged_gqa_decode_fp8kv over seq_lens[b] + seqlen_new keys do, with
+ * mx_paged_gqa_decode_append's arguments plus the two scales.  Up to 16 new tokens it is one
+ * launch: the attention kernel quantizes the new rows, writes them and attends the quantized
+ * values.  Longer appends run the append kernel first.
  * No counterpart in the reference (bf16 caches only).
  */
 int mx_paged_gqa_decode_append_fp8kv(const void* q, const void* k_new, const void* v_new,

@@ -302,6 +302,24 @@ __device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t x) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x, 1.0f, kHi));
 }
 
+// bf16 to fp8 (e4m3fn) for appends into an fp8 cache: four bf16 values (two dwords) as four
+// bytes, each the e4m3fn value nearest to x / scale with the quotient saturated to [-448, 448]
+// (NaN stays NaN).
+__device__ __forceinline__ float fp8_saturate(float v) {
+  return v > 448.f ? 448.f : (v < -448.f ? -448.f : v);  // comparisons pass NaN through
+}
+
+__device__ __forceinline__ uint32_t bf16x4_to_fp8x4(uint32_t lo, uint32_t hi, float scale) {
+  // x / scale is the correctly rounded fp32 quotient (hipcc's default for fp32 division).
+  const float a = fp8_saturate(__uint_as_float(lo << 16) / scale);
+  const float b = fp8_saturate(__uint_as_float(lo & 0xffff0000u) / scale);
+  const float c = fp8_saturate(__uint_as_float(hi << 16) / scale);
+  const float d = fp8_saturate(__uint_as_float(hi & 0xffff0000u) / scale);
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);  // bytes 0, 1
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);       // bytes 2, 3
+  return (uint32_t)w;
+}
+
 template <int D>
 __device__ __forceinline__ void k_lane_offsets8(LaneOffsets& lo, int lane, int kv) {
   constexpr int SPR = D / 16;    // 16-byte segments per fp8 K row
@@ -531,8 +549,9 @@ struct MainShape {
   uint16_t* v_dst;
   int new_tokens;
   // fp8 caches: V values are v_scale times the stored fp8 values (the K scale is folded into
-  // scale_log2 on the host).
+  // scale_log2 on the host).  k_scale is kept for the fused append, which quantizes new keys.
   float v_scale;
+  float k_scale;
 };
 
 // fp8 caches: a wave's output accumulators were built from unscaled V; O is linear in V, so
@@ -929,6 +948,7 @@ __device__ __forceinline__ SeqExtent seq_extent(const int32_t* seq_lens, int b,
 // slot written is read unmasked by the launch (cache chunks cover positions below `cache`).
 // With head_dim 256 the chunk runs after the ring instead and the cache is written by
 // copy_new_tokens at the end of the launch.
+template <bool kFp8 = false>
 struct NewTokens {
   const MainShape& sh;
   int b, kv, cache;
@@ -938,16 +958,27 @@ struct NewTokens {
   const int32_t* bt_row;
   uint32_t* status;
 
-  // With head_dim 256 the ring leaves no registers for a chunk in flight beside it: the new
-  // keys are then loaded and processed after the ring (finish).
+  // With head_dim 256 the ring leaves no registers for a chunk in flight beside it, and an
+  // fp8 ring's slots cannot hold bf16 rows: the new keys are then loaded and processed after
+  // the ring (finish).
   template <int D>
-  static constexpr bool kOverlap = D <= 128;
+  static constexpr bool kOverlap = D <= 128 && !kFp8;
+  // bf16 caches at head_dim 256: the cache rows are written after the attention, by
+  // copy_new_tokens.  (fp8 caches: finish writes the quantized rows.)
+  template <int D>
+  static constexpr bool kCopyAfter = D > 128 && !kFp8;
 
   template <int D>
   __device__ __forceinline__ void load(Chunk<D>& c) const {
     if constexpr (kOverlap<D>)
       if (active) load_rows(c);
   }
+  template <int D>
+  __device__ __forceinline__ void load(Chunk8<D>&) const {}
+  template <int D, int KT>
+  __device__ __forceinline__ void process(SoftmaxState<D> (&)[KT], const Chunk8<D>&,
+                                          const bf16x8 (&)[KT][D / 32], const int (&)[KT],
+                                          char*) const {}
   template <int D, int KT>
   __device__ __forceinline__ void process(SoftmaxState<D> (&st)[KT], const Chunk<D>& c,
                                           const bf16x8 (&qop)[KT][D / 32],
@@ -967,7 +998,72 @@ struct NewTokens {
       if (active) {
         Chunk<D> c;
         load_rows(c);
+        if constexpr (kFp8) quantize_and_store(c);
         run(st, c, qop, row_lim, klds);
+      }
+    }
+  }
+
+  // fp8 caches: every bf16 value x of the loaded rows becomes the e4m3fn value q nearest to
+  // x / scale (saturated, as the append kernel stores it); q is written to the row's cache slot
+  // (when this wave writes) and replaces x in the chunk, widened back to bf16, so the new keys
+  // are attended as the cache will hold them (the scales multiply back in the softmax scale
+  // and on the output).
+  template <int D>
+  __device__ __forceinline__ void quantize_and_store(Chunk<D>& c) const {
+    constexpr int VW = D / 16;
+    uint32_t k8[D / 32][2];
+    uint32_t v8[4][VW / 4];
+    const float ks = sh.k_scale, vs = sh.v_scale;
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) {
+      u32x4& w = c.k[i];
+      k8[i][0] = bf16x4_to_fp8x4(w[0], w[1], ks);
+      k8[i][1] = bf16x4_to_fp8x4(w[2], w[3], ks);
+      w = u32x4{fp8x2_to_bf16x2<false>(k8[i][0]), fp8x2_to_bf16x2<true>(k8[i][0]),
+                fp8x2_to_bf16x2<false>(k8[i][1]), fp8x2_to_bf16x2<true>(k8[i][1])};
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int w = 0; w < VW / 4; ++w) {
+        v8[r][w] = bf16x4_to_fp8x4(c.v[r][2 * w], c.v[r][2 * w + 1], vs);
+        c.v[r][2 * w] = fp8x2_to_bf16x2<false>(v8[r][w]);
+        c.v[r][2 * w + 1] = fp8x2_to_bf16x2<true>(v8[r][w]);
+      }
+    if (write) store_rows8<D>(k8, v8);
+  }
+
+  // store_rows for fp8 bytes: K segment i of a lane is 8 bytes at byte 8 * (lane % (D/8)) of
+  // its row, V is VW bytes at byte VW * (lane & 15).
+  template <int D>
+  __device__ __forceinline__ void store_rows8(const uint32_t (&k8)[D / 32][2],
+                                              const uint32_t (&v8)[4][D / 64]) const {
+    int lane = threadIdx.x & 63;
+    asm volatile("" : "+v"(lane));
+    constexpr int SPR = D / 8;
+    constexpr int RPI = 64 / SPR;
+    constexpr int VW = D / 16;
+    uint8_t* kd = reinterpret_cast<uint8_t*>(sh.k_dst);
+    uint8_t* vd = reinterpret_cast<uint8_t*>(sh.v_dst);
+    const RowSlots rs = row_slots<D>();
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) {
+      const int64_t o = rs.slot(i * RPI + lane / SPR);
+      if (o >= 0) *reinterpret_cast<u32x2*>(kd + o + 8 * (lane % SPR)) = u32x2{k8[i][0], k8[i][1]};
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t o = rs.slot(4 * (lane >> 4) + r);
+      if (o >= 0) {
+        uint8_t* dst = vd + o + VW * (lane & 15);
+        if constexpr (D == 64) {
+          *reinterpret_cast<uint32_t*>(dst) = v8[r][0];
+        } else if constexpr (D == 128) {
+          *reinterpret_cast<u32x2*>(dst) = u32x2{v8[r][0], v8[r][1]};
+        } else {
+          *reinterpret_cast<u32x4*>(dst) = u32x4{v8[r][0], v8[r][1], v8[r][2], v8[r][3]};
+        }
       }
     }
   }
@@ -1004,6 +1100,45 @@ struct NewTokens {
   // i*(512/D) + j/(D/8); V: lane (r16, g4) holds elements (D/16)*r16 .. of row 4*g4 + r) go
   // to their page slots.  The S <= 16 <= page_size positions span at most two pages, whose ids
   // are two wave-uniform loads.
+  // Cache slots of the new rows: the S <= 16 <= page_size positions span at most two pages.
+  struct RowSlots {
+    int n_ok, at, psize, page0, pid0, pid1, kvD;
+    bool ok0, ok1;
+    const MainShape* shp;
+    // Element offset of new row j's KV head, or -1 when it is not written.
+    __device__ __forceinline__ int64_t slot(int j) const {
+      const int pos = at + j;
+      const bool first = pos / psize == page0;
+      if (j >= n_ok || !(first ? ok0 : ok1)) return -1;
+      return (int64_t)(first ? pid0 : pid1) * shp->page_stride +
+             (int64_t)(pos % psize) * shp->token_stride + kvD;
+    }
+  };
+  // The two page ids (wave-uniform loads); flags rows past the table row or in pages outside
+  // the pool.
+  template <int D>
+  __device__ __forceinline__ RowSlots row_slots() const {
+    const int lane = threadIdx.x & 63;
+    RowSlots rs;
+    rs.shp = &sh;
+    rs.at = at;
+    rs.kvD = kv * D;
+    rs.psize = kChunk << sh.chunk_shift;
+    const int S = sh.new_tokens;
+    const int table_tokens = sh.max_pages * rs.psize;
+    rs.n_ok = max(0, min(S, table_tokens - at));  // rows whose position is in the row
+    if (rs.n_ok < S && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_SEQ_TOO_LONG);
+    rs.page0 = at / rs.psize;
+    rs.pid0 = rs.n_ok > 0 ? bt_row[rs.page0] : -1;
+    rs.pid1 = rs.n_ok > 0 ? bt_row[(at + rs.n_ok - 1) / rs.psize] : -1;
+    auto valid = [&](int pid) { return pid >= 0 && (sh.num_pages <= 0 || pid < sh.num_pages); };
+    rs.ok0 = valid(rs.pid0);
+    rs.ok1 = valid(rs.pid1);
+    if (rs.n_ok > 0 && !(rs.ok0 && rs.ok1) && lane == 0)
+      atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
+    return rs;
+  }
+
   template <int D>
   __device__ __forceinline__ void store_rows(const Chunk<D>& c) const {
     int lane = threadIdx.x & 63;
@@ -1011,26 +1146,9 @@ struct NewTokens {
     constexpr int SPR = D / 8;
     constexpr int RPI = 64 / SPR;
     constexpr int VW = D / 16;
-    const int S = sh.new_tokens;
-    const int psize = kChunk << sh.chunk_shift;
-    const int table_tokens = sh.max_pages * psize;
-    const int n_ok = max(0, min(S, table_tokens - at));  // rows whose position is in the row
-    if (n_ok < S && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_SEQ_TOO_LONG);
-    if (n_ok == 0) return;
-    const int page0 = at / psize;
-    const int pid0 = bt_row[page0];
-    const int pid1 = bt_row[(at + n_ok - 1) / psize];
-    auto valid = [&](int pid) { return pid >= 0 && (sh.num_pages <= 0 || pid < sh.num_pages); };
-    const bool ok0 = valid(pid0), ok1 = valid(pid1);
-    if (!(ok0 && ok1) && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
-    // Element offset of new row j's KV head kv, or -1 when it is not written.
-    auto slot = [&](int j) -> int64_t {
-      const int pos = at + j;
-      const bool first = pos / psize == page0;
-      if (j >= n_ok || !(first ? ok0 : ok1)) return -1;
-      return (int64_t)(first ? pid0 : pid1) * sh.page_stride +
-             (int64_t)(pos % psize) * sh.token_stride + kv * D;
-    };
+    const RowSlots rs = row_slots<D>();
+    if (rs.n_ok == 0) return;
+    auto slot = [&](int j) -> int64_t { return rs.slot(j); };
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) {
       const int64_t o = slot(i * RPI + lane / SPR);
@@ -1208,7 +1326,6 @@ void mx_paged_decode_splitkv(
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ block_table,
     float* __restrict__ part_o, float* __restrict__ part_lse, uint32_t* __restrict__ counters,
     uint32_t* __restrict__ status, const MainShape sh) {
-  static_assert(!(kAppend && kFp8), "the fused append writes bf16 caches only");
   using L = GroupLds<D, NW, KT>;
   __shared__ __attribute__((aligned(16))) char lds[L::kBytes];
   __shared__ int s_last;
@@ -1250,7 +1367,7 @@ void mx_paged_decode_splitkv(
   // tokens of (b, kv) to the cache, after its share of the attention (and after its arrival at
   // the merge).
   auto copy_if_writer = [&]() {
-    if constexpr (kAppend && !NewTokens::kOverlap<D>)
+    if constexpr (kAppend && NewTokens<kFp8>::template kCopyAfter<D>)
       if (split == 0 && grp == 0)
         copy_new_tokens<D>(seq_lens, block_table, b, kv, sh, status, tid, 64 * NW);
   };
@@ -1266,9 +1383,9 @@ void mx_paged_decode_splitkv(
     // Fused append: the split holding the last schedule chunk also takes the new keys, as one
     // more chunk after its cache chunks in the waves' round-robin order.
     const bool last = c_hi * kChunk >= seq;
-    const NewTokens nt{sh,          b,          kv,    ext.cache, last && wv == (c_end - c_lo) % NW,
+    const NewTokens<kFp8> nt{sh, b, kv, ext.cache, last && wv == (c_end - c_lo) % NW,
                        grp == 0,    ext.at,     bt_row, status};
-    stream_chunks<D, NBUF, NW, kCausal, KT>(st, qop, kc, vc, bt_row, kv, c_lo, c_end, ext.cache,
+    stream_chunks<D, NBUF, NW, kCausal, KT, NewTokens<kFp8>, kFp8>(st, qop, kc, vc, bt_row, kv, c_lo, c_end, ext.cache,
                                             c_mask, row_lim, wv, L::ktile(lds, wv), sh, bad_page,
                                             nt);
   } else {
@@ -1385,7 +1502,6 @@ void mx_paged_decode_balanced(
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ block_table,
     float* __restrict__ part_o, float* __restrict__ part_lse, uint32_t* __restrict__ counters,
     uint32_t* __restrict__ status, const MainShape sh) {
-  static_assert(!(kAppend && kFp8), "the fused append writes bf16 caches only");
   using L = GroupLds<D, NW, KT>;
   __shared__ __attribute__((aligned(16))) char lds[L::kBytes];
   __shared__ int s_int[NW + 4];
@@ -1554,9 +1670,9 @@ void mx_paged_decode_balanced(
       if constexpr (kAppend) {
         // Fused append: the piece holding the unit's last schedule chunk also takes the new
         // keys, as one more chunk after its cache chunks in the waves' round-robin order.
-        const NewTokens nt{sh,       b,      kv,     ext.cache, cb == n_b && wv == (c_end - ca) % NW,
+        const NewTokens<kFp8> nt{sh, b, kv, ext.cache, cb == n_b && wv == (c_end - ca) % NW,
                            grp == 0, ext.at, bt_row, status};
-        stream_chunks<D, NBUF, NW, kCausal, KT>(st, qop, kc, vc, bt_row, kv, ca, c_end,
+        stream_chunks<D, NBUF, NW, kCausal, KT, NewTokens<kFp8>, kFp8>(st, qop, kc, vc, bt_row, kv, ca, c_end,
                                                 ext.cache, c_mask, row_lim, wv,
                                                 L::ktile(lds, wv), sh, bad_page, nt);
       } else {
@@ -1675,7 +1791,7 @@ void mx_paged_decode_balanced(
     }
   }
   if (bad_page && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
-  if constexpr (kAppend && !NewTokens::kOverlap<D>) {
+  if constexpr (kAppend && NewTokens<kFp8>::template kCopyAfter<D>) {
     // Fused append with head_dim 256: the cache writes of the (sequence, KV head) pairs, spread
     // over the workgroups that hold positions, each doing its share after all its pieces.
     const int n_active = (total + qsz - 1) / qsz;
@@ -1875,21 +1991,6 @@ __global__ __launch_bounds__(256) void mx_paged_kv_append_kernel(
 // e4m3fn value nearest to x / scale (ties to even), with x / scale clamped to [-448, 448]
 // first (saturation; NaN stays NaN).  One wave per (new token, K or V); a lane converts 8
 // values per step, one 16-byte load of bf16 into one 8-byte store of fp8.
-__device__ __forceinline__ float fp8_saturate(float v) {
-  return v > 448.f ? 448.f : (v < -448.f ? -448.f : v);  // comparisons pass NaN through
-}
-
-__device__ __forceinline__ uint32_t bf16x4_to_fp8x4(uint32_t lo, uint32_t hi, float scale) {
-  // x / scale is the correctly rounded fp32 quotient (hipcc's default for fp32 division).
-  const float a = fp8_saturate(__uint_as_float(lo << 16) / scale);
-  const float b = fp8_saturate(__uint_as_float(lo & 0xffff0000u) / scale);
-  const float c = fp8_saturate(__uint_as_float(hi << 16) / scale);
-  const float d = fp8_saturate(__uint_as_float(hi & 0xffff0000u) / scale);
-  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);  // bytes 0, 1
-  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);       // bytes 2, 3
-  return (uint32_t)w;
-}
-
 __global__ __launch_bounds__(256) void mx_paged_kv_append_fp8_kernel(
     const uint16_t* __restrict__ k_new, const uint16_t* __restrict__ v_new,
     uint8_t* __restrict__ k_cache, uint8_t* __restrict__ v_cache,
@@ -2283,6 +2384,7 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   sh.cap_tokens = (int)plan.cap_tokens;
   sh.scale_log2 = scale * 1.4426950408889634f * (kv.fp8 ? kv.k_scale : 1.0f);
   sh.v_scale = kv.fp8 ? kv.v_scale : 1.0f;
+  sh.k_scale = kv.fp8 ? kv.k_scale : 1.0f;
   sh.num_splits = (int)plan.splits;
   sh.fused_combine = 0;
   sh.tokens_per_split = (int)plan.tokens_per_split;
@@ -2302,7 +2404,7 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   // The fused-append variants of the main kernels load the new keys in the LDS-staged K layout.
   constexpr bool kCanAppend = k_via_lds<D>();
   const bool append = app.new_tokens > 0;
-  if (append && (!kCanAppend || kv.fp8)) return hipErrorInvalidValue;
+  if (append && !kCanAppend) return hipErrorInvalidValue;
   const uint16_t* q16 = static_cast<const uint16_t*>(q);
   const uint16_t* k16 = static_cast<const uint16_t*>(k);
   const uint16_t* v16 = static_cast<const uint16_t*>(v);
@@ -2319,7 +2421,9 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
                          reinterpret_cast<float*>(ws + plan.lse_offset),
                          reinterpret_cast<uint32_t*>(ws + plan.counter_offset), status, sh);
     };
-    if (kv.fp8)
+    if (kv.fp8 && append)
+      go(mx_paged_decode_balanced<D, kNBUF8, kNW, kCausal, KT, kCanAppend, true>, k8, v8);
+    else if (kv.fp8)
       go(mx_paged_decode_balanced<D, kNBUF8, kNW, kCausal, KT, false, true>, k8, v8);
     else if (append)
       go(mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, kCanAppend, false>, k16, v16);
@@ -2346,7 +2450,9 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
                          static_cast<uint16_t*>(out), seq_lens, block_table, part_o, part_lse,
                          reinterpret_cast<uint32_t*>(ws + kStatusBytes), status, sh);
     };
-    if (kv.fp8)
+    if (kv.fp8 && append)
+      go(mx_paged_decode_splitkv<D, kNBUF8, kNW, kCausal, KT, kCanAppend, true>, k8, v8);
+    else if (kv.fp8)
       go(mx_paged_decode_splitkv<D, kNBUF8, kNW, kCausal, KT, false, true>, k8, v8);
     else if (append)
       go(mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT, kCanAppend, false>, k16, v16);
@@ -2795,15 +2901,14 @@ static int decode_append_impl(const void* q, const void* k_new, const void* v_ne
   const bool lds_k = kh.head_dim == 64    ? k_via_lds<64>()
                      : kh.head_dim == 128 ? k_via_lds<128>()
                                           : k_via_lds<256>();
-  if (seqlen_new >= 1 && seqlen_new <= kChunk && lds_k && !kv.fp8) {
+  if (seqlen_new >= 1 && seqlen_new <= kChunk && lds_k) {
     // One launch: the new keys are one extra chunk of each unit, written to the cache by the
     // wave that loads them.
     app.new_tokens = (int)seqlen_new;
     app.k_new = k_new;
     app.v_new = v_new;
   } else if (seqlen_new > 0) {
-    // Longer appends, and every append into an fp8 cache: the append kernel first, then the
-    // decode over seq_lens + seqlen_new.
+    // Longer appends: the append kernel first, then the decode over seq_lens + seqlen_new.
     st = launch_append(k_new, v_new, k_cache, v_cache, seq_lens, block_table, batch, seqlen_new,
                        num_kv_heads, head_dim, page_size, num_pages, max_pages_per_seq,
                        workspace, stream, kv);

@@ -369,7 +369,7 @@ def paged_gqa_decode_append(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.T
     For S <= 16 the append and the attention are one kernel launch (the new keys are read from
     k_new / v_new as one more chunk and written to the cache by the same kernel); longer
     appends run the append kernel first.  float8_e4m3fn caches take per-tensor scales (see
-    paged_kv_append and paged_gqa_decode) and always run the append kernel first.
+    paged_kv_append and paged_gqa_decode); their new rows are attended as quantized.
     """
     args, out, fp8 = _append_call_args(q, k_new, v_new, k_cache, v_cache, block_table,
                                        seq_lens, scale, out, causal, num_splits, max_seq_len,

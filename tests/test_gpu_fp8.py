@@ -245,11 +245,13 @@ def test_fp8_append_flags_and_skips_bad_slots():
 
 
 @pytest.mark.parametrize("S,SQ,causal,ns", [(1, 1, False, 0), (3, 3, True, 0), (1, 1, False, 5),
-                                            (20, 4, True, -3)])
-@pytest.mark.parametrize("D,Hq,Hkv", [(128, 32, 8), (64, 16, 2)])
+                                            (16, 2, True, 0), (20, 4, True, -3), (7, 1, False, 24)])
+@pytest.mark.parametrize("D,Hq,Hkv", [(128, 32, 8), (64, 16, 2), (256, 16, 2)])
 def test_fp8_decode_append_matches_the_oracle(S, SQ, causal, ns, D, Hq, Hkv):
-    """Append-and-attend on an fp8 cache: the quantized append, then the fp8 decode over
-    L + S keys; the caches bit-exact, the output within the tolerance; the bound call equal."""
+    """Append-and-attend on an fp8 cache: up to 16 new tokens in one launch (the kernel
+    quantizes them, writes the bytes and attends the quantized values), more as the append
+    kernel then the decode over L + S keys; the caches bit-exact, the output within the
+    tolerance; the bound call equal."""
     from mx_flash_attn_kernel_opt__amd import BoundDecodeAppend, paged_gqa_decode_append
     from oracle import paged_kv_append_reference
     B, P = 3, 16
@@ -283,3 +285,25 @@ def test_fp8_decode_append_matches_the_oracle(S, SQ, causal, ns, D, Hq, Hkv):
     assert torch.equal(out2.cpu(), out.cpu()), label
     assert torch.equal(kd2.cpu().view(torch.uint8), kr.view(torch.uint8)), label
     assert read_device_status() == 0
+
+
+def test_fp8_fused_append_flags_and_skips_bad_slots():
+    """The one-launch path on an fp8 cache skips and flags new rows whose slot is past the
+    table row or in a page outside the pool, like the append kernel."""
+    from mx_flash_attn_kernel_opt__amd import _lib, paged_gqa_decode_append
+    from oracle import paged_kv_append_reference
+    B, S, Hq, Hkv, D, P = 3, 4, 16, 4, 128, 16
+    kn, vn, k8, v8, table, lens = _append_case(B, S, Hkv, D, P, 2, seed=11, specials=False)
+    table[1, 1] = 10_000
+    lens[:] = torch.tensor([0, 14, 30], dtype=torch.int32)
+    q = (torch.randn(B, Hq, D, generator=torch.Generator().manual_seed(2)) * 0.5).to(
+        torch.bfloat16)
+    kd, vd = k8.to(DEV), v8.to(DEV)
+    paged_gqa_decode_append(q.to(DEV), kn.to(DEV), (vn.float() * 0.25).to(torch.bfloat16).to(DEV),
+                            kd, vd, table.to(DEV), lens.to(DEV), k_scale=0.5, v_scale=2.0)
+    flags = read_device_status()
+    assert flags & _lib.MX_DEVICE_BAD_PAGE_ID and flags & _lib.MX_DEVICE_SEQ_TOO_LONG
+    kr, vr, _ = paged_kv_append_reference(kn, (vn.float() * 0.25).to(torch.bfloat16), k8, v8,
+                                          table, lens, k_scale=0.5, v_scale=2.0)
+    assert torch.equal(kd.cpu().view(torch.uint8), kr.view(torch.uint8))
+    assert torch.equal(vd.cpu().view(torch.uint8), vr.view(torch.uint8))
