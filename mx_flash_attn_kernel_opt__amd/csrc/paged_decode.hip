@@ -31,6 +31,9 @@
 //  * Paged K/V append (mx_paged_kv_append), and append-and-attend (mx_paged_gqa_decode_append):
 //    for up to 16 new tokens the kernels' kAppend variants read the new keys from k_new / v_new
 //    as one extra chunk per unit and write them to their cache slots in the same launch.
+//  * fp8 (e4m3fn) caches with per-tensor scales (the _fp8kv entries; kFp8 variants): chunks of
+//    one-byte K/V widened to bf16 on the way into the MFMA operands; head_dim-64 heads run in
+//    adjacent pairs as heads of dim 128 (MainShape::pair_group); appends quantize on write.
 
 #include <hip/hip_runtime.h>
 
