@@ -55,9 +55,11 @@ extern "C" {
 #define MX_DEVICE_SEQ_TOO_LONG 2u   /* seq_lens[b] exceeded the capacity the call was planned for */
 
 /* Schedules reported by mx_paged_gqa_decode_plan. */
-#define MX_SCHEDULE_SPLIT_GRID 0   /* grid (Hkv * row groups, batch, splits); with 2-16 splits
-                                      the last split of each unit merges, above 16 a combine
-                                      kernel follows                                              */
+#define MX_SCHEDULE_SPLIT_GRID 0   /* grid (Hkv * row groups, batch, splits); the splits of
+                                      each unit merge through an in-kernel tree of arrival
+                                      counters, or, when batch * Hkv * row groups *
+                                      ceil(splits / 16) > 12288, in a combine kernel that
+                                      follows                                                     */
 #define MX_SCHEDULE_BALANCED 1     /* one launch of a fixed number of workgroups that divide the
                                       batch's K/V chunks evenly from seq_lens on the device and
                                       merge split sequences themselves                            */
@@ -112,7 +114,10 @@ void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_pa
  *   workspace          device memory of >= mx_paged_gqa_decode_workspace_size() bytes,
  *                      zero-filled once by the caller before first use (its first 196 864
  *                      bytes hold a status word and merge counters that every call leaves at
- *                      zero); NULL = library-owned.
+ *                      zero); NULL = library-owned: one per device, grown on demand
+ *                      (doubling; earlier allocations are kept, never freed, so graphs
+ *                      captured with them stay valid).  A call that needs it to grow fails
+ *                      with MX_STATUS_INVALID_ARGUMENT on a capturing stream.
  *   phase              0, MX_PHASE_MAIN_ONLY or MX_PHASE_COMBINE_ONLY.
  *   stream             hipStream_t (NULL = legacy default stream).
  * q, k_cache and v_cache must be 16-byte aligned and out 8-byte aligned (MX_STATUS_INVALID_ARGUMENT

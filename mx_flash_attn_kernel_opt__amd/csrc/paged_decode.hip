@@ -22,10 +22,11 @@
 //    chunk max exceeds it by more than 8); the final O / l uses one max for both, so it is
 //    exact.  Masked chunks (sequence tail, causal limits) use selects, never arithmetic on
 //    unused page slots.
-//  * Two schedules: the split grid (Hkv * row groups, batch, splits), whose last split per unit
-//    merges the partials in-kernel (up to 16 splits; a combine kernel above that), and a single
+//  * Two schedules, both one launch: the split grid (Hkv * row groups, batch, splits), whose
+//    splits merge their partials through an in-kernel tree of arrival counters (fan-in 16; a
+//    combine kernel in a second launch only when the counters do not fit), and a
 //    length-balanced launch that cuts the batch's chunk line into equal shares on the device
-//    and merges cut units through a fan-in-8 tree of arrival counters.
+//    and merges cut units through a fan-in-8 tree of the same kind.
 //  * Sharded decode: the same kernels can write each query row as fp32 output plus its
 //    log-sum-exp (mx_paged_gqa_decode_partial) for a cross-device merge (mx_lse_merge).
 //  * Paged K/V append (mx_paged_kv_append), and append-and-attend (mx_paged_gqa_decode_append):
@@ -49,6 +50,7 @@
 #include <vector>
 
 #include "mx_paged_decode.h"
+#include "positions.h"
 
 namespace {
 
@@ -102,81 +104,37 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
 }
 
-// Compile-time tuning knobs (defaults are the measured best on MI355X).
-#ifndef MX_NBUF_D64
-#define MX_NBUF_D64 2
-#endif
-#ifndef MX_NBUF_D128
-#define MX_NBUF_D128 2
-#endif
-#ifndef MX_NBUF_D256
-#define MX_NBUF_D256 1
-#endif
-#ifndef MX_K_NONTEMPORAL
-#define MX_K_NONTEMPORAL 1
-#endif
-#ifndef MX_V_NONTEMPORAL
-#define MX_V_NONTEMPORAL 1
-#endif
-#ifndef MX_K_VIA_LDS_D64
-#define MX_K_VIA_LDS_D64 1
-#endif
-#ifndef MX_K_VIA_LDS_D128
-#define MX_K_VIA_LDS_D128 1
-#endif
-#ifndef MX_K_VIA_LDS_D256
-#define MX_K_VIA_LDS_D256 1
-#endif
-#ifndef MX_NW_D64
-#define MX_NW_D64 2
-#endif
-#ifndef MX_NW_D128
-#define MX_NW_D128 4
-#endif
-#ifndef MX_NW_D256
-#define MX_NW_D256 4
-#endif
-// Minimum waves per SIMD the register allocator must allow (1 = no cap).
-#ifndef MX_WAVES_PER_EU_D64
-#define MX_WAVES_PER_EU_D64 2
-#endif
-#ifndef MX_WAVES_PER_EU_D128
-#define MX_WAVES_PER_EU_D128 2
-#endif
-#ifndef MX_WAVES_PER_EU_D256
-#define MX_WAVES_PER_EU_D256 1
-#endif
-
+// Shapes of the main kernels, each the best of interleaved A/B runs on MI355X:
+//  * chunks in a wave's register ring (bf16 caches): 2 at head_dim 64 and 128, 1 at 256.  D=64
+//    with 3 or 4 chunks ran 189-190 against 172 us, D=256 with 2 ran 178.5 against 174.9 us,
+//    and D=128 with 3 or 4 (one wave per SIMD) stayed within 1 % everywhere;
+//  * waves per workgroup: 2 at head_dim 64, 4 at 128 and 256.  D=64 with 4 waves ran 176.5
+//    against 172 us, D=128 with 8 gained nothing, D=256 with 8 spilled to scratch (302 us);
+//  * waves per SIMD the register allocation must leave room for: 2, or 1 at head_dim 256.
 template <int D>
 constexpr int ring_depth() {
-  return D == 64 ? MX_NBUF_D64 : (D == 128 ? MX_NBUF_D128 : MX_NBUF_D256);
+  return D == 256 ? 1 : 2;
 }
 
-// Whether K chunks are staged through LDS (see k_lane_offsets).
-template <int D>
-constexpr bool k_via_lds() {
-  return (D == 64 ? MX_K_VIA_LDS_D64 : (D == 128 ? MX_K_VIA_LDS_D128 : MX_K_VIA_LDS_D256)) != 0;
-}
-
-// Waves per workgroup of the main kernels (split grid and balanced schedule).
 template <int D>
 constexpr int waves_per_group() {
-  return D == 64 ? MX_NW_D64 : (D == 128 ? MX_NW_D128 : MX_NW_D256);
+  return D == 64 ? 2 : 4;
 }
 
-// K/V stream loads: wave-uniform base plus per-lane byte offset.  NT selects the
-// nontemporal (streaming) cache policy.
-template <bool NT>
+template <int D, int KT>
+constexpr int min_waves_per_simd() {
+  return (KT == 2 || D == 256) ? 1 : 2;  // two row tiles hold two states: one wave per SIMD
+}
+
+// K/V stream loads: wave-uniform base plus per-lane byte offset, nontemporal (K/V are streamed
+// once: the device's streaming-read rate rises from 6.1-6.4 to 7.15 TB/s with the hint).
 __device__ __forceinline__ u32x4 ld_kv16(const uint16_t* base, uint32_t byte_off) {
   const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + byte_off);
-  if constexpr (NT) return __builtin_nontemporal_load(p);
-  return *p;
+  return __builtin_nontemporal_load(p);
 }
-template <bool NT>
 __device__ __forceinline__ u32x2 ld_kv8(const uint16_t* base, uint32_t byte_off) {
   const u32x2* p = reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(base) + byte_off);
-  if constexpr (NT) return __builtin_nontemporal_load(p);
-  return *p;
+  return __builtin_nontemporal_load(p);
 }
 
 // Register image of one 16-token chunk of one KV head.
@@ -192,13 +150,13 @@ template <int D>
 __device__ __forceinline__ void load_v_row(uint32_t (&dst)[D / 32], const uint16_t* base,
                                            uint32_t byte_off) {
   if constexpr (D == 64) {
-    const u32x2 x = ld_kv8<MX_V_NONTEMPORAL != 0>(base, byte_off);
+    const u32x2 x = ld_kv8(base, byte_off);
     dst[0] = x[0];
     dst[1] = x[1];
   } else {
 #pragma unroll
     for (int w = 0; w < D / 32; w += 4) {
-      const u32x4 x = ld_kv16<MX_V_NONTEMPORAL != 0>(base, byte_off + 4 * w);
+      const u32x4 x = ld_kv16(base, byte_off + 4 * w);
       dst[w + 0] = x[0];
       dst[w + 1] = x[1];
       dst[w + 2] = x[2];
@@ -215,13 +173,12 @@ struct LaneOffsets {
   uint32_t token_bytes;   // bytes between consecutive tokens of a page
 };
 
-// K chunk staging.  Direct (k_via_lds<D>() false): lane (r16, g4) loads K[r16][32i + 8g4 .. +7]
-// straight into the MFMA A operand: each load instruction touches 16 rows x 64 B.
-// Through LDS (k_via_lds<D>() true): lane j loads row i*RPI + j/SPR, 16-byte segment j%SPR of
-// the chunk (RPI = 512/D whole 2D-byte rows per instruction, the V access pattern), writes it
-// to a wave-private 16 x 2D-byte LDS tile at an XOR-swizzled segment, and reads the A operand
+// K chunk staging through LDS: lane j loads row i*RPI + j/SPR, 16-byte segment j%SPR of the
+// chunk (RPI = 512/D whole 2D-byte rows per instruction, the V access pattern), writes it to a
+// wave-private 16 x 2D-byte LDS tile at an XOR-swizzled segment, and reads the MFMA A operand
 // back with ds_read_b128; the swizzle keeps both the writes and the 16 rows of one read
-// conflict-free.
+// conflict-free.  (Loading the A operand directly, 16 rows x 64 B per instruction, streamed at
+// 5.8 TB/s against 6.6 TB/s for whole nontemporal rows, and config 2 ran 177.6 us against 169.9.)
 template <int D>
 __device__ __forceinline__ int k_swizzle(int row) {
   return D == 64 ? ((row >> 1) & 7) : (row & 15);
@@ -229,15 +186,10 @@ __device__ __forceinline__ int k_swizzle(int row) {
 
 template <int D>
 __device__ __forceinline__ void k_lane_offsets(LaneOffsets& lo, int lane, int kv) {
-  if constexpr (k_via_lds<D>()) {
-    constexpr int SPR = D / 8;     // 16-byte segments per K row
-    constexpr int RPI = 64 / SPR;  // rows per load instruction
-    lo.k = (uint32_t)(lane / SPR) * lo.token_bytes + 2u * (uint32_t)(kv * D) + 16u * (lane % SPR);
-    lo.k_step = RPI * lo.token_bytes;
-  } else {
-    lo.k = (uint32_t)(lane & 15) * lo.token_bytes + 2u * (uint32_t)(kv * D) + 16u * (lane >> 4);
-    lo.k_step = 64u;
-  }
+  constexpr int SPR = D / 8;     // 16-byte segments per K row
+  constexpr int RPI = 64 / SPR;  // rows per load instruction
+  lo.k = (uint32_t)(lane / SPR) * lo.token_bytes + 2u * (uint32_t)(kv * D) + 16u * (lane % SPR);
+  lo.k_step = RPI * lo.token_bytes;
 }
 
 // Loads all 16 token rows of a chunk.  A chunk never crosses a page (page_size % 16 == 0),
@@ -247,8 +199,7 @@ template <int D>
 __device__ __forceinline__ void load_chunk(Chunk<D>& c, const uint16_t* kpage,
                                            const uint16_t* vpage, const LaneOffsets& lo) {
 #pragma unroll
-  for (int i = 0; i < D / 32; ++i)
-    c.k[i] = ld_kv16<MX_K_NONTEMPORAL != 0>(kpage, lo.k + (uint32_t)i * lo.k_step);
+  for (int i = 0; i < D / 32; ++i) c.k[i] = ld_kv16(kpage, lo.k + (uint32_t)i * lo.k_step);
 #pragma unroll
   for (int r = 0; r < 4; ++r) load_v_row<D>(c.v[r], vpage, lo.v + r * lo.token_bytes);
 }
@@ -257,29 +208,22 @@ __device__ __forceinline__ void load_chunk(Chunk<D>& c, const uint16_t* kpage,
 template <int D>
 __device__ __forceinline__ void k_operands(bf16x8 (&kop)[D / 32], const Chunk<D>& c,
                                            char* klds, int lane) {
-  if constexpr (k_via_lds<D>()) {
-    constexpr int SPR = D / 8;
-    constexpr int RPI = 64 / SPR;
-    const int wr = lane / SPR;
-    const int ws = lane % SPR;
+  constexpr int SPR = D / 8;
+  constexpr int RPI = 64 / SPR;
+  const int wr = lane / SPR;
+  const int ws = lane % SPR;
 #pragma unroll
-    for (int i = 0; i < D / 32; ++i) {
-      const int row = i * RPI + wr;
-      *reinterpret_cast<u32x4*>(klds + row * 2 * D + 16 * (ws ^ k_swizzle<D>(row))) = c.k[i];
-    }
-    const int t = lane & 15;
-    const int g4 = lane >> 4;
-#pragma unroll
-    for (int i = 0; i < D / 32; ++i)
-      kop[i] = __builtin_bit_cast(
-          bf16x8, *reinterpret_cast<const u32x4*>(klds + t * 2 * D +
-                                                  16 * ((4 * i + g4) ^ k_swizzle<D>(t))));
-  } else {
-    (void)klds;
-    (void)lane;
-#pragma unroll
-    for (int i = 0; i < D / 32; ++i) kop[i] = __builtin_bit_cast(bf16x8, c.k[i]);
+  for (int i = 0; i < D / 32; ++i) {
+    const int row = i * RPI + wr;
+    *reinterpret_cast<u32x4*>(klds + row * 2 * D + 16 * (ws ^ k_swizzle<D>(row))) = c.k[i];
   }
+  const int t = lane & 15;
+  const int g4 = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i)
+    kop[i] = __builtin_bit_cast(
+        bf16x8, *reinterpret_cast<const u32x4*>(klds + t * 2 * D +
+                                                16 * ((4 * i + g4) ^ k_swizzle<D>(t))));
 }
 
 // ------------------------------------------------------------------------------------------
@@ -337,20 +281,19 @@ __device__ __forceinline__ void load_chunk(Chunk8<D>& c, const uint8_t* kpage,
   const uint16_t* kp = reinterpret_cast<const uint16_t*>(kpage);
   const uint16_t* vp = reinterpret_cast<const uint16_t*>(vpage);
 #pragma unroll
-  for (int i = 0; i < D / 64; ++i)
-    c.k[i] = ld_kv16<MX_K_NONTEMPORAL != 0>(kp, lo.k + (uint32_t)i * lo.k_step);
+  for (int i = 0; i < D / 64; ++i) c.k[i] = ld_kv16(kp, lo.k + (uint32_t)i * lo.k_step);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const uint32_t off = lo.v + r * lo.token_bytes;
     if constexpr (D == 64) {
       const uint32_t* p = reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(vp) + off);
-      c.v[r][0] = MX_V_NONTEMPORAL ? __builtin_nontemporal_load(p) : *p;
+      c.v[r][0] = __builtin_nontemporal_load(p);
     } else if constexpr (D == 128) {
-      const u32x2 x = ld_kv8<MX_V_NONTEMPORAL != 0>(vp, off);
+      const u32x2 x = ld_kv8(vp, off);
       c.v[r][0] = x[0];
       c.v[r][1] = x[1];
     } else {
-      const u32x4 x = ld_kv16<MX_V_NONTEMPORAL != 0>(vp, off);
+      const u32x4 x = ld_kv16(vp, off);
       c.v[r][0] = x[0];
       c.v[r][1] = x[1];
       c.v[r][2] = x[2];
@@ -365,7 +308,6 @@ __device__ __forceinline__ void load_chunk(Chunk8<D>& c, const uint8_t* kpage,
 template <int D>
 __device__ __forceinline__ void k_operands(bf16x8 (&kop)[D / 32], const Chunk8<D>& c,
                                            char* klds, int lane) {
-  static_assert(k_via_lds<D>(), "fp8 K chunks are staged through LDS");
   constexpr int SPR = D / 16;
   constexpr int RPI = 64 / SPR;
   const int wr = lane / SPR;
@@ -528,7 +470,8 @@ struct MainShape {
   // split grid
   int num_splits;
   int tokens_per_split;  // multiple of page_size
-  int fused_combine;     // split grid: the last split of each unit merges the partials itself
+  int fused_combine;     // split grid: the splits of each unit merge their partials in-kernel
+  int split_groups;      // split grid: ceil(num_splits / kSplitFanIn), merge counters per unit
   // balanced schedule
   int num_groups;        // workgroups of the launch
   int unit_overhead;     // positions charged per (sequence, KV head) on top of its chunks
@@ -571,7 +514,7 @@ __device__ __forceinline__ void scale_o_by_v_scale(SoftmaxState<D> (&st)[KT],
 // Keys of sequence b before clamping (see MainShape::appended).
 __device__ __forceinline__ int key_count(const int32_t* seq_lens, int b, int appended) {
   const int L = seq_lens[b];
-  return appended > 0 ? max(L, 0) + appended : L;
+  return appended > 0 ? keys_after_append(L, appended) : L;
 }
 
 // Sequence length as the kernels see it: clamped to the planned capacity (flagged).
@@ -800,7 +743,7 @@ template <int D, int NW, int KT>
 struct GroupLds {
   static constexpr int kRows = 16 * KT;
   static constexpr int kRow = D + 4;
-  static constexpr int kKTile = k_via_lds<D>() ? 16 * 2 * D : 16;
+  static constexpr int kKTile = 16 * 2 * D;
   static constexpr int kMergeBytes = NW * kRows * kRow * 4 + 2 * NW * kRows * 4;
   static constexpr int kBytes = (NW * kKTile > kMergeBytes) ? NW * kKTile : kMergeBytes;
   __device__ __forceinline__ static char* ktile(char* base, int wv) { return base + wv * kKTile; }
@@ -1073,7 +1016,6 @@ struct NewTokens {
 
   template <int D>
   __device__ __forceinline__ void load_rows(Chunk<D>& c) const {
-    static_assert(k_via_lds<D>(), "the fused append loads K in the LDS-staged layout");
     // An opaque copy of the lane index: keeps the per-lane offsets of this rarely taken block
     // from being hoisted out of the callers' loops, where they would stay live (and spill)
     // across the streaming of every chunk.
@@ -1110,9 +1052,10 @@ struct NewTokens {
     const MainShape* shp;
     // Element offset of new row j's KV head, or -1 when it is not written.
     __device__ __forceinline__ int64_t slot(int j) const {
+      if (j >= n_ok) return -1;  // (at + j is formed only inside the table row)
       const int pos = at + j;
       const bool first = pos / psize == page0;
-      if (j >= n_ok || !(first ? ok0 : ok1)) return -1;
+      if (!(first ? ok0 : ok1)) return -1;
       return (int64_t)(first ? pid0 : pid1) * shp->page_stride +
              (int64_t)(pos % psize) * shp->token_stride + kvD;
     }
@@ -1209,11 +1152,11 @@ __device__ __forceinline__ void copy_new_tokens(const int32_t* __restrict__ seq_
     const int is_v = e >= S * SEG;
     const int j = (e - is_v * S * SEG) / SEG;
     const int seg = e % SEG;
-    if (at >= table_tokens - j) {  // at + j past the table row (no int overflow)
+    const int pos = append_position(at, j, table_tokens);
+    if (pos < 0) {  // past the table row
       overflow = true;
       continue;
     }
-    const int pos = at + j;
     const int pid = bt_row[pos / psize];
     if (pid < 0 || (sh.num_pages > 0 && pid >= sh.num_pages)) {
       bad = true;
@@ -1231,77 +1174,200 @@ __device__ __forceinline__ void copy_new_tokens(const int32_t* __restrict__ seq_
     atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
 }
 
-constexpr int kMergeFanIn = 8;   // partials merged per step of a cross-workgroup merge
+// Partials merged per step of a cross-workgroup merge tree: the balanced schedule's pieces, and
+// the split grid's splits.
+constexpr int kPieceFanIn = 8;
+constexpr int kSplitFanIn = 16;
 
-// Cross-workgroup handoff of partials.  Device-scoped accesses (MX_MERGE_SCOPED_ACCESS = 1):
-// partials are stored and loaded with agent-scope atomic accesses (write-through / coherent at
-// the device, sc1), each wave waits for its own stores to complete before the workgroup barrier
-// and the arrival counter; no L2 write-back or invalidate is needed.  Fenced (0): plain
-// accesses bracketed by __threadfence() in every thread (an L2 write-back per wave).
-#ifndef MX_MERGE_SCOPED_ACCESS
-#define MX_MERGE_SCOPED_ACCESS 1
-#endif
-
+// Cross-workgroup handoff of partials (the split grid's in-kernel merge and the balanced
+// kernel's merge tree).  Partials are stored and loaded with relaxed agent-scope atomic
+// accesses, which keep each location coherent across the device's XCDs with no L2 write-back
+// (gfx950: global_store / global_load with sc1).  The order between the stores of the pieces
+// and the loads of the workgroup that merges them comes from the arrival counter (arrive_last).
+// A plain-store variant with __threadfence() in every thread was measured first: it writes back
+// the L2 per wave, and config 2 with 1 024 workgroups ran 505 us instead of 174.
 __device__ __forceinline__ void store_partial4(float* p, f32x4 v) {
-#if MX_MERGE_SCOPED_ACCESS
   const u32x4 u = __builtin_bit_cast(u32x4, v);
   const uint64_t lo = (uint64_t)u[0] | ((uint64_t)u[1] << 32);
   const uint64_t hi = (uint64_t)u[2] | ((uint64_t)u[3] << 32);
   __hip_atomic_store(reinterpret_cast<uint64_t*>(p), lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __hip_atomic_store(reinterpret_cast<uint64_t*>(p) + 1, hi, __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
-#else
-  *reinterpret_cast<f32x4*>(p) = v;
-#endif
 }
 __device__ __forceinline__ void store_partial1(float* p, float v) {
-#if MX_MERGE_SCOPED_ACCESS
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#else
-  *p = v;
-#endif
 }
 __device__ __forceinline__ f32x4 load_partial4(const float* p) {
-#if MX_MERGE_SCOPED_ACCESS
   const uint64_t lo = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
                                         __HIP_MEMORY_SCOPE_AGENT);
   const uint64_t hi = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p) + 1,
                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const u32x4 u = {(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
   return __builtin_bit_cast(f32x4, u);
-#else
-  return *reinterpret_cast<const f32x4*>(p);
-#endif
 }
 __device__ __forceinline__ float load_partial1(const float* p) {
-#if MX_MERGE_SCOPED_ACCESS
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#else
-  return *p;
-#endif
 }
-// Makes this thread's partial stores visible device-wide before the arrival count.
-__device__ __forceinline__ void publish_partials() {
-#if MX_MERGE_SCOPED_ACCESS
+
+// Arrival of this workgroup at `counter`, which `expected` workgroups reach once each; returns,
+// uniformly over the workgroup, whether it arrived last (and then resets the counter for the
+// next call).  Called by every thread after its partial stores.  The steps:
+//  1. each wave waits until its own stores have completed (s_waitcnt vmcnt(0));
+//  2. the barrier: every wave of the workgroup is past step 1 before thread 0 goes on, so the
+//     stores happen before its increment;
+//  3. thread 0 increments with an agent-scope acq_rel read-modify-write.  Its release half
+//     orders the workgroup's stores before the increment; the acquire half orders the
+//     increments of the earlier arrivals (and so their stores) before what follows;
+//  4. the barrier hands thread 0's result, and the acquire, to every thread before any loads
+//     the last arrival makes of the others' partials.
+__device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected, int* s_flag) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);  // every store of this wave has completed
+  __builtin_amdgcn_s_waitcnt(0);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
-#else
-  __threadfence();
-#endif
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = prev == expected - 1;
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_flag = last ? 1 : 0;
+  }
+  __syncthreads();
+  return *s_flag != 0;
 }
-// Orders the partial loads after the arrival count that proved them complete.
-__device__ __forceinline__ void acquire_partials() {
-#if MX_MERGE_SCOPED_ACCESS
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-#else
-  __threadfence();
-#endif
+
+// One merge step of a cross-workgroup merge tree: the gsize (<= W) items of a group, at level-0
+// slots gslot + t * stride, merged as
+//   O = sum_t 2^(lse_t - M) O_t / sum_t 2^(lse_t - M),  lse = M + log2 sum_t 2^(lse_t - M),
+// M = max_t lse_t (optimized_c500_flash_attn.cu:666-728, log2 domain).  A row no item saw a key
+// for (every lse -inf: causal rows before their first key) stays zeros with lse -inf.  Each
+// thread issues the loads of all items for its dims at once (unconditional: slots past the
+// group re-read its first item and are masked by their lse), so a step is one memory round
+// trip.  The merged rows go to the output (`final`) or to the group's first slot (lse to s_lse,
+// which the caller stores after a barrier).
+template <int D, int NW, int W, class Tree>
+__device__ __forceinline__ void merge_group(const Tree& tree, int gslot, int stride, int gsize,
+                                            int nrows, bool final, float* s_lse) {
+  // An opaque copy of the thread index: keeps the per-thread addressing of this step from being
+  // hoisted out of the callers' loops, where it would stay live across the chunk streaming.
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  for (int e = tid; e < nrows * (D / 4); e += 64 * NW) {
+    const int hh = e / (D / 4);
+    const int d = 4 * (e - hh * (D / 4));
+    float ls[W];
+    f32x4 vs[W];
+#pragma unroll
+    for (int t = 0; t < W; ++t) {
+      const int sl = gslot + (t < gsize ? t : 0) * stride;
+      ls[t] = load_partial1(tree.lse(hh, sl));
+      vs[t] = load_partial4(tree.o(hh, sl) + d);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < W; ++t) {
+      if (t >= gsize) ls[t] = -INFINITY;
+      mx = fmaxf(mx, ls[t]);
+    }
+    const bool seen = mx > -INFINITY;
+    const float mref = seen ? mx : 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    float wsum = 0.f;
+#pragma unroll
+    for (int t = 0; t < W; ++t) {
+      const float w = __builtin_amdgcn_exp2f(ls[t] - mref);  // 0 for t >= gsize
+      wsum += w;
+      acc += w * vs[t];
+    }
+    acc *= seen ? 1.0f / wsum : 0.f;
+    const float lse = seen ? mx + log2f(wsum) : -INFINITY;
+    if (final) {
+      tree.store(hh, d, acc, lse);
+    } else {
+      store_partial4(tree.o(hh, gslot) + d, acc);
+      if (d == 0) s_lse[hh] = lse;
+    }
+  }
+}
+
+// The merge tree of one cut unit: the balanced schedule's pieces, or the split grid's splits.
+// Level-0 item i is the partial that workgroup has stored for it (normalised O / l per row and
+// its log2-sum-exp); level-l item j covers level-0 items [j*F^l, (j+1)*F^l) and is stored in the
+// slot of its first one.  The last arrival of each group of up to F items merges them
+// (merge_group, with as many loads per thread as the group has items, rounded up to a power of
+// two) into the group's slot, or into the output when it is the last level's only group.
+// Returns when this workgroup is not the last arrival of its group, or after the output is
+// written.
+//
+// `tree` provides o(hh, slot) / lse(hh, slot) (the fp32 partial row hh of a level-0 slot and its
+// log2-sum-exp), counter(level, slot) (the arrival counter of the level's group whose first item
+// is at `slot`) and store(hh, d, o, lse) (the final store of dims d..d+3 of row hh).  s_lse holds
+// nrows floats.
+template <int D, int NW, int F, class Tree>
+__device__ __forceinline__ void merge_tree(const Tree& tree, int item, int nitems, int nrows,
+                                           float* s_lse, int* s_flag) {
+  static_assert(F == 8 || F == 16, "fan-in of the merge trees");
+  const int tid = threadIdx.x;
+  int stride = 1;  // level-0 items per item of this level
+  for (int level = 0;; ++level) {
+    const int grp = item / F;
+    const int gsize = min(F, nitems - grp * F);
+    const int gslot = grp * F * stride;  // level-0 slot of the group's first item
+    if (!arrive_last(tree.counter(level, gslot), (uint32_t)gsize, s_flag)) return;
+    const int nnext = (nitems + F - 1) / F;
+    const bool final = nnext == 1;
+    if (gsize <= 2) {
+      merge_group<D, NW, 2>(tree, gslot, stride, gsize, nrows, final, s_lse);
+    } else if (gsize <= 4) {
+      merge_group<D, NW, 4>(tree, gslot, stride, gsize, nrows, final, s_lse);
+    } else if (F == 8 || gsize <= 8) {
+      merge_group<D, NW, 8>(tree, gslot, stride, gsize, nrows, final, s_lse);
+    } else {
+      merge_group<D, NW, F>(tree, gslot, stride, gsize, nrows, final, s_lse);
+    }
+    if (final) return;
+    // Every thread has read the group's log-sum-exps before the merged one overwrites the first.
+    __syncthreads();
+    if (tid < nrows) store_partial1(tree.lse(tid, gslot), s_lse[tid]);
+    item = grp;
+    nitems = nnext;
+    stride *= F;
+  }
 }
 
 // ------------------------------------------------------------------------------------------
 // Split-grid kernel
 // ------------------------------------------------------------------------------------------
+
+// The split grid's merge tree over the splits of one unit (merge_tree).  Partials are row-major
+// over the query rows with the splits innermost: part_o[(row * num_splits + split) * D + d],
+// part_lse[row * num_splits + split] (the layout mx_paged_decode_combine reads).  Each level of
+// the counter region holds split_groups = ceil(num_splits / kSplitFanIn) counters per unit.
+template <int D>
+struct SplitTree {
+  const MainShape& sh;
+  float* part_o;
+  float* part_lse;
+  uint32_t* counters;
+  uint16_t* out;
+  int64_t rbase;  // row_base of the unit
+  int r0;         // first row of the unit's row group
+  int unit;       // (sequence, KV head and row group) index
+  __device__ __forceinline__ int64_t row(int hh) const { return rbase + row_offset(r0 + hh, sh); }
+  __device__ __forceinline__ float* o(int hh, int slot) const {
+    return part_o + (row(hh) * sh.num_splits + slot) * D;
+  }
+  __device__ __forceinline__ float* lse(int hh, int slot) const {
+    return part_lse + row(hh) * sh.num_splits + slot;
+  }
+  __device__ __forceinline__ uint32_t* counter(int level, int slot) const {
+    return counters + (int64_t)level * kMaxSlots + (int64_t)unit * sh.split_groups +
+           slot / kSplitFanIn;
+  }
+  __device__ __forceinline__ void store(int hh, int d, f32x4 v, float l) const {
+    store_row4<D>(out, sh, row(hh), d, v, l);
+  }
+};
 
 // Grid (Hkv * row_tiles, batch, splits), NW waves per workgroup, row_tiles groups of KT 16-row
 // tiles per KV head.  Consecutive workgroup ids, which the dispatcher deals round-robin to the
@@ -1316,12 +1382,12 @@ __device__ __forceinline__ void acquire_partials() {
 // through LDS.  KT = 2 holds two tiles' states per wave, so one wave per SIMD (512 registers).
 //
 // A sequence cut into several splits leaves one normalised partial (O/l, log2-sum-exp) per
-// split and row.  With fused_combine the last split of each unit to finish (a device-scope
-// arrival counter per unit) merges them itself, so the whole call is one launch; otherwise
-// mx_paged_decode_combine merges them in a second launch.
+// split and row.  With fused_combine the splits of each unit merge them through an in-kernel
+// tree (merge_tree: groups of kSplitFanIn splits, the last arrival of a group merges it), so the
+// whole call is one launch; otherwise mx_paged_decode_combine merges them in a second launch.
 template <int D, int NBUF, int NW, bool kCausal, int KT, bool kAppend, bool kFp8>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
-    KT == 2 ? 1 : (D == 64 ? MX_WAVES_PER_EU_D64 : (D == 128 ? MX_WAVES_PER_EU_D128 : MX_WAVES_PER_EU_D256)))))
+__global__ __launch_bounds__(64 * NW)
+__attribute__((amdgpu_waves_per_eu(min_waves_per_simd<D, KT>())))
 void mx_paged_decode_splitkv(
     const uint16_t* __restrict__ q, CachePtr<kAppend, CacheElem<kFp8>> kc,
     CachePtr<kAppend, CacheElem<kFp8>> vc,
@@ -1332,6 +1398,7 @@ void mx_paged_decode_splitkv(
   using L = GroupLds<D, NW, KT>;
   __shared__ __attribute__((aligned(16))) char lds[L::kBytes];
   __shared__ int s_last;
+  __shared__ float s_lse[16 * KT];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   // Wave index, made provably wave-uniform so the chunk indices derived from it stay in
@@ -1420,63 +1487,11 @@ void mx_paged_decode_splitkv(
     return;
   }
 
-  // Arrival of this split; the unit's last split merges all of them.
+  // This split's partial is level-0 item `split` of the unit's merge tree.
   const int nsv = (seq + sh.tokens_per_split - 1) / sh.tokens_per_split;  // splits with tokens
-  uint32_t* counter = counters + (int64_t)b * gridDim.x + blockIdx.x;
-  publish_partials();
-  __syncthreads();
-  if (tid == 0) s_last = (atomicAdd(counter, 1u) == (uint32_t)(nsv - 1)) ? 1 : 0;
-  __syncthreads();
-  if (!s_last) {
-    copy_if_writer();
-    return;
-  }
-  if (tid == 0) *counter = 0u;  // ready for the next call
-  acquire_partials();
-  // out[row] = sum_s 2^(lse_s - M) O_s / sum_s 2^(lse_s - M), M = max_s lse_s; a causal row no
-  // split saw a key for (every lse -inf) stays zeros.
-  // One online pass, the loads of kMergeFanIn splits issued together per round.
-  for (int e = tid; e < nrows * (D / 4); e += 64 * NW) {
-    const int hh = e / (D / 4);
-    const int d = 4 * (e - hh * (D / 4));
-    const int64_t row = row_base(b, kv, sh) + row_offset(r0 + hh, sh);
-    const float* lse = part_lse + row * sh.num_splits;
-    const float* po = part_o + row * sh.num_splits * D + d;
-    float mx = -INFINITY;  // running max of the log2-sum-exps seen
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    float wsum = 0.f;
-    for (int s0 = 0; s0 < nsv; s0 += kMergeFanIn) {
-      float ls[kMergeFanIn];
-      f32x4 vs[kMergeFanIn];
-#pragma unroll
-      for (int t = 0; t < kMergeFanIn; ++t) {  // unconditional loads, extra slots masked
-        const int sl = min(s0 + t, nsv - 1);
-        ls[t] = load_partial1(lse + sl);
-        vs[t] = load_partial4(po + (int64_t)sl * D);
-      }
-#pragma unroll
-      for (int t = 0; t < kMergeFanIn; ++t)
-        if (s0 + t >= nsv) ls[t] = -INFINITY;
-      float bm = mx;
-#pragma unroll
-      for (int t = 0; t < kMergeFanIn; ++t) bm = fmaxf(bm, ls[t]);
-      if (bm > -INFINITY) {
-        const float a = __builtin_amdgcn_exp2f(mx - bm);  // 0 while nothing was seen
-        acc *= a;
-        wsum *= a;
-#pragma unroll
-        for (int t = 0; t < kMergeFanIn; ++t) {
-          const float w = __builtin_amdgcn_exp2f(ls[t] - bm);
-          wsum += w;
-          acc += w * vs[t];
-        }
-        mx = bm;
-      }
-    }
-    const bool seen = wsum > 0.f;
-    store_row4<D>(out, sh, row, d, acc * (seen ? 1.0f / wsum : 0.f),
-                  seen ? mx + log2f(wsum) : -INFINITY);
-  }
+  const SplitTree<D> tree{sh,  part_o, part_lse, counters, out, row_base(b, kv, sh), r0,
+                          b * (int)gridDim.x + (int)blockIdx.x};
+  merge_tree<D, NW, kSplitFanIn>(tree, split, nsv, nrows, s_lse, &s_last);
   copy_if_writer();
 }
 
@@ -1484,7 +1499,34 @@ void mx_paged_decode_splitkv(
 // Length-balanced kernel
 // ------------------------------------------------------------------------------------------
 
-constexpr int kMergeLevels = 4;  // enough for 8^4 = 4096 pieces per unit
+// The balanced schedule's merge tree over the pieces of one unit (merge_tree).  Piece k of a unit
+// whose first piece is held by workgroup w0 has slot slot0 + k, slot0 = w0 + unit index: the
+// slots of different units are disjoint, and so are the counters (kCounterLevels levels of 8,
+// enough for 8^4 = 4096 pieces per unit), indexed like the slots.  A slot holds tile_rows rows.
+template <int D>
+struct BalancedTree {
+  const MainShape& sh;
+  float* part_o;
+  float* part_lse;
+  uint32_t* counters;
+  uint16_t* out;
+  int64_t rbase;  // row_base of the unit
+  int r0;         // first row of the unit's row group
+  int slot0;
+  int tile_rows;
+  __device__ __forceinline__ float* o(int hh, int slot) const {
+    return part_o + ((int64_t)(slot0 + slot) * tile_rows + hh) * D;
+  }
+  __device__ __forceinline__ float* lse(int hh, int slot) const {
+    return part_lse + (int64_t)(slot0 + slot) * tile_rows + hh;
+  }
+  __device__ __forceinline__ uint32_t* counter(int level, int slot) const {
+    return counters + (int64_t)level * kMaxSlots + slot0 + slot;
+  }
+  __device__ __forceinline__ void store(int hh, int d, f32x4 v, float l) const {
+    store_row4<D>(out, sh, rbase + row_offset(r0 + hh, sh), d, v, l);
+  }
+};
 
 // One launch of num_groups workgroups covers the whole batch whatever the length mix.  Every
 // (sequence b, KV head and row group j) "unit" with n_b = ceil(L_b/16) > 0 chunks occupies n_b +
@@ -1496,8 +1538,8 @@ constexpr int kMergeLevels = 4;  // enough for 8^4 = 4096 pieces per unit
 // a normalised partial (O/l, log2-sum-exp) to its own slot, and the last piece to finish
 // merges them through a fan-in-8 tree of per-unit counters, so the whole call is one launch.
 template <int D, int NBUF, int NW, bool kCausal, int KT, bool kAppend, bool kFp8>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
-    KT == 2 ? 1 : (D == 64 ? MX_WAVES_PER_EU_D64 : (D == 128 ? MX_WAVES_PER_EU_D128 : MX_WAVES_PER_EU_D256)))))
+__global__ __launch_bounds__(64 * NW)
+__attribute__((amdgpu_waves_per_eu(min_waves_per_simd<D, KT>())))
 void mx_paged_decode_balanced(
     const uint16_t* __restrict__ q, CachePtr<kAppend, CacheElem<kFp8>> kc,
     CachePtr<kAppend, CacheElem<kFp8>> vc,
@@ -1643,7 +1685,6 @@ void mx_paged_decode_balanced(
   int span = n_b + alpha;
   int j = (x_begin - seq_start) / span;  // (KV head, row group) of the unit
   int u0 = seq_start + j * span;  // first position of unit (b, j)
-  const int per_level = kMaxSlots;  // counters of merge level l start at l * kMaxSlots
   bool bad_page = false;
 
   for (;;) {
@@ -1695,10 +1736,9 @@ void mx_paged_decode_balanced(
           store_row4<D>(out, sh, rbase + row_offset(r0 + hh, sh), d, o, lse);
         }
       } else {
-        // Piece k of the unit goes to slot slot0 + k; level-l item j of the merge tree covers
-        // pieces [j*8^l, (j+1)*8^l) and lives in the slot of its first piece.
+        // Piece k of the unit goes to slot slot0 + k and is level-0 item k of its merge tree.
         const int slot0 = first_wg + unit;
-        int item = wg - first_wg;
+        const int item = wg - first_wg;
         {
           float* po = part_o + (int64_t)(slot0 + item) * TR * D;
           float* pl = part_lse + (int64_t)(slot0 + item) * TR;
@@ -1710,72 +1750,8 @@ void mx_paged_decode_balanced(
             if (d == 0) store_partial1(pl + hh, lse);
           }
         }
-        int nitems = npieces;
-        int stride = 1;  // pieces per item at this level
-        for (int level = 0; level < kMergeLevels; ++level) {
-          const int grp = item / kMergeFanIn;
-          const int gsize = min(kMergeFanIn, nitems - grp * kMergeFanIn);
-          const int gslot = slot0 + grp * kMergeFanIn * stride;
-          // Publish this workgroup's stores device-wide, then count arrivals of the group.
-          publish_partials();
-          __syncthreads();
-          if (tid == 0) {
-            const uint32_t prev = atomicAdd(&counters[level * per_level + gslot], 1u);
-            s_int[NW + 2] = (prev == (uint32_t)(gsize - 1)) ? 1 : 0;
-          }
-          __syncthreads();
-          if (!s_int[NW + 2]) break;  // another piece of the group is still running
-          if (tid == 0) counters[level * per_level + gslot] = 0u;  // ready for the next call
-          acquire_partials();
-          const int nnext = (nitems + kMergeFanIn - 1) / kMergeFanIn;
-          // Merge items grp*8 .. grp*8+gsize-1 (slots gslot + t*stride).
-          for (int e = tid; e < nrows * (D / 4); e += 64 * NW) {
-            const int hh = e / (D / 4);
-            const int d = 4 * (e - hh * (D / 4));
-            float mx = -INFINITY;
-            // All log-sum-exps and partial vectors of the group are loaded in one round.
-            float lses[kMergeFanIn];
-            f32x4 vals[kMergeFanIn];
-#pragma unroll
-            for (int t = 0; t < kMergeFanIn; ++t) {  // unconditional loads, extra slots masked
-              const int64_t sl = gslot + min(t, gsize - 1) * stride;
-              lses[t] = load_partial1(part_lse + sl * TR + hh);
-              vals[t] = load_partial4(part_o + (sl * TR + hh) * D + d);
-            }
-#pragma unroll
-            for (int t = 0; t < kMergeFanIn; ++t)
-              if (t >= gsize) lses[t] = -INFINITY;
-#pragma unroll
-            for (int t = 0; t < kMergeFanIn; ++t) mx = fmaxf(mx, lses[t]);
-            // A row no piece of the group saw a key for (every lse -inf) stays zeros with
-            // log2-sum-exp -inf: its weights are exp2(-inf) = 0 against a reference of 0.
-            const bool seen = mx > -INFINITY;
-            const float mref = seen ? mx : 0.f;
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            float wsum = 0.f;
-#pragma unroll
-            for (int t = 0; t < kMergeFanIn; ++t) {
-              const float w = __builtin_amdgcn_exp2f(lses[t] - mref);  // 0 for t >= gsize
-              wsum += w;
-              acc += w * vals[t];
-            }
-            acc *= seen ? 1.0f / wsum : 0.f;
-            const float lse = seen ? mx + log2f(wsum) : -INFINITY;
-            if (nnext == 1) {
-              store_row4<D>(out, sh, rbase + row_offset(r0 + hh, sh), d, acc, lse);
-            } else {
-              store_partial4(part_o + ((int64_t)gslot * TR + hh) * D + d, acc);
-              if (d == 0) s_lse[hh] = lse;
-            }
-          }
-          if (nnext == 1) break;
-          // Every thread has read the group's log-sum-exps before any is overwritten.
-          __syncthreads();
-          if (tid < nrows) store_partial1(part_lse + (int64_t)gslot * TR + tid, s_lse[tid]);
-          item = grp;
-          nitems = nnext;
-          stride *= kMergeFanIn;
-        }
+        const BalancedTree<D> tree{sh, part_o, part_lse, counters, out, rbase, r0, slot0, TR};
+        merge_tree<D, NW, kPieceFanIn>(tree, item, npieces, nrows, s_lse, &s_int[NW + 2]);
       }
       // The merged states in LDS share bytes with the K tiles the next piece streams into:
       // no wave may start that piece until every wave has finished reading them.
@@ -1974,8 +1950,8 @@ __global__ __launch_bounds__(256) void mx_paged_kv_append_kernel(
   const bool is_v = (wave & 1) != 0;
   const int b = tok / seqlen_new;
   const int j = tok - b * seqlen_new;
-  const int pos = max(seq_lens[b], 0) + j;
-  if (pos >= max_pages * page_size) {
+  const int pos = append_position(seq_lens[b], j, max_pages * page_size);
+  if (pos < 0) {
     if (lane == 0 && !is_v) atomicOr(status, (uint32_t)MX_DEVICE_SEQ_TOO_LONG);
     return;
   }
@@ -2007,8 +1983,8 @@ __global__ __launch_bounds__(256) void mx_paged_kv_append_fp8_kernel(
   const bool is_v = (wave & 1) != 0;
   const int b = tok / seqlen_new;
   const int j = tok - b * seqlen_new;
-  const int pos = max(seq_lens[b], 0) + j;
-  if (pos >= max_pages * page_size) {
+  const int pos = append_position(seq_lens[b], j, max_pages * page_size);
+  if (pos < 0) {
     if (lane == 0 && !is_v) atomicOr(status, (uint32_t)MX_DEVICE_SEQ_TOO_LONG);
     return;
   }
@@ -2071,16 +2047,22 @@ constexpr int64_t kMaxGridDim = 65535;
 constexpr int64_t kMaxGroup = 128;
 constexpr int64_t kBalancedMinUnits = 64;
 constexpr int64_t kBalancedMinCap = 2048;  // tokens of capacity (max_seq_len) for balanced
-constexpr int64_t kFusedMaxSplits = 16;  // split grid: merge in-kernel up to this many splits
 constexpr int64_t kMaxMergeRows = int64_t(1) << 25;  // mx_lse_merge: 64 * rows work-items < 2^31
 
 int64_t groups_per_cu(int64_t head_dim) { return head_dim == 64 ? 2 : 1; }
 
+// Whether the split grid's units merge their splits in-kernel (one launch): each level of the
+// counter region must hold ceil(splits / kSplitFanIn) counters per unit.  Otherwise the combine
+// kernel merges in a second launch.
+bool split_tree_fits(int64_t units, int64_t splits) {
+  return units * ceil_div(splits, kSplitFanIn) <= kMaxSlots;
+}
+
+// Balanced schedule: chunk positions charged per unit on top of its chunks, for its query load
+// and pipeline fill (2 -> 6 took ragged decode from 115 to 84 us; 8-16 moved it by < 1 %).
+constexpr int kUnitOverhead = 6;
 // Balanced schedule limits: the largest batch whose seq_lens scan stays within two passes of
-// one workgroup; the per-unit overhead (chunk positions) is MX_UNIT_OVERHEAD.
-#ifndef MX_UNIT_OVERHEAD
-#define MX_UNIT_OVERHEAD 6
-#endif
+// one workgroup.
 constexpr int64_t kBalancedMaxBatch = 512;
 constexpr int64_t kBalancedMaxGroups = 4095;  // pieces per unit stay within the 8^4 merge tree
 constexpr int64_t kBalancedMaxUnits = 8192;   // batch * Hkv * row tiles (counter region)
@@ -2161,8 +2143,10 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
   plan->row_tiles = row_tiles;
   plan->tiles_per_group = tiles_per_group;
   if (num_heads > kMaxGridDim) return fail(MX_STATUS_UNSUPPORTED, "num_heads must be <= 65535");
-  if (max_pages > (int64_t)INT32_MAX / page_size)
-    return fail(MX_STATUS_UNSUPPORTED, "max_pages_per_seq * page_size must fit in int32");
+  // Token positions are int32, including a capacity plus the up to 16 keys a one-launch
+  // append-and-attend adds.
+  if (max_pages > ((int64_t)INT32_MAX - kChunk) / page_size)
+    return fail(MX_STATUS_UNSUPPORTED, "max_pages_per_seq * page_size must be < 2^31 - 16");
   if (num_kv_heads * head_dim * page_size > (int64_t)INT32_MAX / 4)
     return fail(MX_STATUS_UNSUPPORTED, "page too large for 32-bit in-page offsets");
 
@@ -2205,7 +2189,7 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
   plan->chunk_shift = shift;
   const int64_t units = batch * num_kv_heads * row_tiles;
   const bool balanced_ok = batch <= kBalancedMaxBatch && units <= kBalancedMaxUnits &&
-                           units * (ceil_div(cap, kChunk) + MX_UNIT_OVERHEAD) < kBalancedMaxLine;
+                           units * (ceil_div(cap, kChunk) + kUnitOverhead) < kBalancedMaxLine;
   // Short capacities favour one split per unit (no length scan, no merge): the balanced
   // schedule pays off from 2 048 tokens, or from 1 024 with at least 512 units.
   const bool long_enough = cap >= kBalancedMinCap || (cap >= kBalancedMinCap / 2 && units >= 512);
@@ -2252,15 +2236,20 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
   return MX_STATUS_OK;
 }
 
-// Library-owned workspace, one per device, grow-only (as submission_clean.cu:478-491).
+// Library-owned workspace, one per device, grow-only (as submission_clean.cu:478-491).  A grown
+// workspace never frees its predecessors: kernels still in flight, and HIP graphs captured with
+// the old address, keep valid memory until the process ends.  Growth doubles the size, so the
+// retired allocations add up to less than the current one.  A call that grows it starts a fresh
+// device status word.
 struct DeviceWorkspace {
   void* ptr = nullptr;
   int64_t bytes = 0;
+  std::vector<void*> retired;
 };
 std::mutex g_ws_mu;
 std::vector<DeviceWorkspace> g_ws;
 
-int internal_workspace(int64_t need, void** out) {
+int internal_workspace(int64_t need, hipStream_t stream, void** out) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) {
     (void)hipGetLastError();
@@ -2270,13 +2259,17 @@ int internal_workspace(int64_t need, void** out) {
   if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1);
   DeviceWorkspace& ws = g_ws[dev];
   if (ws.ptr == nullptr || ws.bytes < need) {
-    const int64_t bytes = std::max<int64_t>(need, 1 << 20);
-    if (ws.ptr != nullptr) {
-      (void)hipDeviceSynchronize();
-      (void)hipFree(ws.ptr);
-      ws.ptr = nullptr;
-      ws.bytes = 0;
+    // Allocating (and clearing) cannot be captured into a graph.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (stream != nullptr && hipStreamIsCapturing(stream, &capture) != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(MX_STATUS_HIP_ERROR, "hipStreamIsCapturing failed");
     }
+    if (capture != hipStreamCaptureStatusNone)
+      return fail(MX_STATUS_INVALID_ARGUMENT,
+                  "the library's workspace must grow, which cannot happen under stream capture: "
+                  "pass a workspace, or make one call of this shape before capturing");
+    const int64_t bytes = std::max<int64_t>({need, 2 * ws.bytes, int64_t(1) << 20});
     void* p = nullptr;
     if (hipMalloc(&p, (size_t)bytes) != hipSuccess || p == nullptr) {
       (void)hipGetLastError();
@@ -2288,6 +2281,7 @@ int internal_workspace(int64_t need, void** out) {
       (void)hipFree(p);
       return fail(MX_STATUS_HIP_ERROR, "hipMemset of the internal workspace failed");
     }
+    if (ws.ptr != nullptr) ws.retired.push_back(ws.ptr);
     ws.ptr = p;
     ws.bytes = bytes;
   }
@@ -2312,18 +2306,13 @@ struct KvFormat {
   float v_scale = 1.0f;
 };
 
-// Whether bf16 caches of head_dim 64 also run as paired heads (KernelHeads).  Off: a bf16 row of
-// 64 dims is a whole line already, and pairing measured 171.1 -> 168.8 us on B=128, Hkv=4,
-// L=8192, within the spread of repeated runs.
-#ifndef MX_PAIR_BF16
-#define MX_PAIR_BF16 0
-#endif
-
 // KV heads as the kernels see them.  Stored heads of dim 64 run in adjacent pairs as kernel heads
 // of dim 128 (MainShape::pair_group) when a head's query rows fit one 16-row tile, so that a
 // pair is still one pass over its K/V.  For fp8 caches this is what makes the reads whole: an
 // fp8 row of 64 dims is half a 128-byte line, which the workgroups of the two unpaired heads
-// each fetch in full (FETCH_SIZE read 2.0x the cache bytes).
+// each fetch in full (FETCH_SIZE read 2.0x the cache bytes).  bf16 caches are not paired: a bf16
+// row of 64 dims is a whole line already, and pairing measured 171.1 -> 168.8 us on B=128,
+// Hkv=4, L=8192, within the spread of repeated runs.
 struct KernelHeads {
   int64_t kv_heads;
   int64_t head_dim;
@@ -2332,7 +2321,7 @@ struct KernelHeads {
 
 KernelHeads kernel_heads(int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads,
                          int64_t head_dim, bool fp8) {
-  const bool pair = (fp8 || MX_PAIR_BF16) && head_dim == 64 && num_kv_heads >= 2 &&
+  const bool pair = fp8 && head_dim == 64 && num_kv_heads >= 2 &&
                     num_kv_heads % 2 == 0 && num_heads % num_kv_heads == 0 && seqlen_q >= 1 &&
                     seqlen_q <= 16 && seqlen_q * (num_heads / num_kv_heads) <= 16;
   if (!pair) return {num_kv_heads, head_dim, 0};
@@ -2342,18 +2331,9 @@ KernelHeads kernel_heads(int64_t seqlen_q, int64_t num_heads, int64_t num_kv_hea
 // Register ring depth of the fp8 kernels (an fp8 chunk takes half the registers of a bf16 one).
 // (A/B on 512 MB fp8 caches, chunks per ring 2/3/4/6: D=64 173.6/174.7/183.0/186.2 us, D=128
 // config-2 shape 95.8/93.2/95.7/96.4 us, D=256 1/2/3/6 chunks 94.5/93.3-96.7/94.9/104.1 us.)
-#ifndef MX_NBUF8_D64
-#define MX_NBUF8_D64 2
-#endif
-#ifndef MX_NBUF8_D128
-#define MX_NBUF8_D128 3
-#endif
-#ifndef MX_NBUF8_D256
-#define MX_NBUF8_D256 1
-#endif
 template <int D>
 constexpr int ring_depth_fp8() {
-  return D == 64 ? MX_NBUF8_D64 : (D == 128 ? MX_NBUF8_D128 : MX_NBUF8_D256);
+  return D == 64 ? 2 : (D == 128 ? 3 : 1);
 }
 
 template <int D, bool kCausal, int KT>
@@ -2390,9 +2370,10 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   sh.k_scale = kv.fp8 ? kv.k_scale : 1.0f;
   sh.num_splits = (int)plan.splits;
   sh.fused_combine = 0;
+  sh.split_groups = 1;
   sh.tokens_per_split = (int)plan.tokens_per_split;
   sh.num_groups = (int)plan.groups;
-  sh.unit_overhead = MX_UNIT_OVERHEAD;
+  sh.unit_overhead = kUnitOverhead;
   sh.num_slots = (int)plan.slots;
   sh.o_out = o_out;
   sh.lse_out = lse_out;
@@ -2404,10 +2385,7 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   sh.k_dst = app.new_tokens > 0 ? static_cast<uint16_t*>(const_cast<void*>(k)) : nullptr;
   sh.v_dst = app.new_tokens > 0 ? static_cast<uint16_t*>(const_cast<void*>(v)) : nullptr;
   uint32_t* status = reinterpret_cast<uint32_t*>(ws);
-  // The fused-append variants of the main kernels load the new keys in the LDS-staged K layout.
-  constexpr bool kCanAppend = k_via_lds<D>();
   const bool append = app.new_tokens > 0;
-  if (append && !kCanAppend) return hipErrorInvalidValue;
   const uint16_t* q16 = static_cast<const uint16_t*>(q);
   const uint16_t* k16 = static_cast<const uint16_t*>(k);
   const uint16_t* v16 = static_cast<const uint16_t*>(v);
@@ -2425,11 +2403,11 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
                          reinterpret_cast<uint32_t*>(ws + plan.counter_offset), status, sh);
     };
     if (kv.fp8 && append)
-      go(mx_paged_decode_balanced<D, kNBUF8, kNW, kCausal, KT, kCanAppend, true>, k8, v8);
+      go(mx_paged_decode_balanced<D, kNBUF8, kNW, kCausal, KT, true, true>, k8, v8);
     else if (kv.fp8)
       go(mx_paged_decode_balanced<D, kNBUF8, kNW, kCausal, KT, false, true>, k8, v8);
     else if (append)
-      go(mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, kCanAppend, false>, k16, v16);
+      go(mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, true, false>, k16, v16);
     else
       go(mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, false, false>, k16, v16);
     return hipGetLastError();
@@ -2437,13 +2415,11 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
 
   float* part_lse = plan.splits > 1 ? reinterpret_cast<float*>(ws + plan.lse_offset) : nullptr;
   float* part_o = plan.splits > 1 ? reinterpret_cast<float*>(ws + plan.o_offset) : nullptr;
-  // One launch (the last split of each unit merges) for up to kFusedMaxSplits splits, when the
-  // units' arrival counters fit the counter region and the caller did not ask for the two
-  // phases separately.  With more splits the merging workgroup's chain of rounds costs more
-  // than a second launch whose many workgroups merge rows in parallel (measured: tiny 10.3 ->
-  // 8.9 us fused at 4 splits; 64 splits 31.1 -> 33.0 us).
-  const bool fused = phase == 0 && plan.splits > 1 && plan.splits <= kFusedMaxSplits &&
-                     batch * num_kv_heads * plan.row_tiles <= kMaxSlots;
+  // One launch (the splits of each unit merge through an in-kernel tree) when the units' arrival
+  // counters fit the counter region and the caller did not ask for the two phases separately.
+  const bool fused = phase == 0 && plan.splits > 1 &&
+                     split_tree_fits(batch * num_kv_heads * plan.row_tiles, plan.splits);
+  sh.split_groups = (int)ceil_div(plan.splits, kSplitFanIn);
   sh.fused_combine = fused ? 1 : 0;
   if (phase != MX_PHASE_COMBINE_ONLY) {
     const dim3 grid((unsigned)(num_kv_heads * plan.row_tiles), (unsigned)batch,
@@ -2454,11 +2430,11 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
                          reinterpret_cast<uint32_t*>(ws + kStatusBytes), status, sh);
     };
     if (kv.fp8 && append)
-      go(mx_paged_decode_splitkv<D, kNBUF8, kNW, kCausal, KT, kCanAppend, true>, k8, v8);
+      go(mx_paged_decode_splitkv<D, kNBUF8, kNW, kCausal, KT, true, true>, k8, v8);
     else if (kv.fp8)
       go(mx_paged_decode_splitkv<D, kNBUF8, kNW, kCausal, KT, false, true>, k8, v8);
     else if (append)
-      go(mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT, kCanAppend, false>, k16, v16);
+      go(mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT, true, false>, k16, v16);
     else
       go(mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT, false, false>, k16, v16);
     const hipError_t e = hipGetLastError();
@@ -2557,7 +2533,7 @@ int prepare_decode(const void* q, const void* k_cache, const void* v_cache, cons
                    int64_t head_dim, int64_t page_size, int64_t num_pages,
                    int64_t max_pages_per_seq, int64_t max_seq_len, int32_t causal, float scale,
                    int64_t num_splits, void** workspace, int64_t workspace_bytes,
-                   int32_t phase, Plan* plan) {
+                   int32_t phase, void* stream, Plan* plan) {
   if (phase != 0 && phase != MX_PHASE_MAIN_ONLY && phase != MX_PHASE_COMBINE_ONLY)
     return fail(MX_STATUS_INVALID_ARGUMENT, "phase must be 0, 1 or 2");
   // The kernels read q, K and V rows as 16-byte vectors and write out in 8-byte pieces.
@@ -2579,7 +2555,7 @@ int prepare_decode(const void* q, const void* k_cache, const void* v_cache, cons
                       std::to_string(plan->workspace_bytes));
     return MX_STATUS_OK;
   }
-  return internal_workspace(plan->workspace_bytes, workspace);
+  return internal_workspace(plan->workspace_bytes, static_cast<hipStream_t>(stream), workspace);
 }
 
 // Launches a prepared decode: bf16 into out, or (partial outputs) fp32 rows into o_out and
@@ -2634,7 +2610,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* o
   const int st = prepare_decode(q, k_cache, v_cache, out, batch, seqlen_q, num_heads,
                                 kh.kv_heads, kh.head_dim, page_size, num_pages, max_pages_per_seq,
                                 max_seq_len, causal, scale, num_splits, &workspace,
-                                workspace_bytes, phase, &plan);
+                                workspace_bytes, phase, stream, &plan);
   if (st != MX_STATUS_OK) return st;
   return run_decode(plan, q, k_cache, v_cache, out, o_out, lse_out, seq_lens, block_table, batch,
                     seqlen_q, num_heads, kh.kv_heads, kh.head_dim, page_size, num_pages,
@@ -2837,11 +2813,11 @@ void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_pa
 
 int mx_read_device_status(void* workspace, int32_t reset, void* stream, int32_t* flags_out) {
   if (!flags_out) return fail(MX_STATUS_NULL_POINTER, "flags_out must be non-NULL");
+  hipStream_t s = static_cast<hipStream_t>(stream);
   if (workspace == nullptr) {
-    int st = internal_workspace(kStatusBytes, &workspace);
+    int st = internal_workspace(kStatusBytes, s, &workspace);
     if (st != MX_STATUS_OK) return st;
   }
-  hipStream_t s = static_cast<hipStream_t>(stream);
   uint32_t word = 0;
   if (hipMemcpyAsync(&word, workspace, sizeof(word), hipMemcpyDeviceToHost, s) != hipSuccess ||
       hipStreamSynchronize(s) != hipSuccess) {
@@ -2870,7 +2846,7 @@ static int kv_append_impl(const void* k_new, const void* v_new, void* k_cache, v
   if (st != MX_STATUS_OK) return st;
   if (seqlen_new == 0) return ok();
   if (workspace == nullptr) {
-    st = internal_workspace(kStatusBytes, &workspace);
+    st = internal_workspace(kStatusBytes, static_cast<hipStream_t>(stream), &workspace);
     if (st != MX_STATUS_OK) return st;
   }
   return launch_append(k_new, v_new, k_cache, v_cache, seq_lens, block_table, batch, seqlen_new,
@@ -2898,13 +2874,10 @@ static int decode_append_impl(const void* q, const void* k_new, const void* v_ne
   const KernelHeads kh = kernel_heads(seqlen_q, num_heads, num_kv_heads, head_dim, kv.fp8);
   st = prepare_decode(q, k_cache, v_cache, out, batch, seqlen_q, num_heads, kh.kv_heads,
                       kh.head_dim, page_size, num_pages, max_pages_per_seq, max_seq_len, causal,
-                      scale, num_splits, &workspace, workspace_bytes, 0, &plan);
+                      scale, num_splits, &workspace, workspace_bytes, 0, stream, &plan);
   if (st != MX_STATUS_OK) return st;
   AppendArgs app;
-  const bool lds_k = kh.head_dim == 64    ? k_via_lds<64>()
-                     : kh.head_dim == 128 ? k_via_lds<128>()
-                                          : k_via_lds<256>();
-  if (seqlen_new >= 1 && seqlen_new <= kChunk && lds_k) {
+  if (seqlen_new >= 1 && seqlen_new <= kChunk) {
     // One launch: the new keys are one extra chunk of each unit, written to the cache by the
     // wave that loads them.
     app.new_tokens = (int)seqlen_new;

@@ -168,6 +168,14 @@ EXTRA = {
     "specdec8_llama3_8b": DecodeSpec(
         "specdec8_llama3_8b", 64, 32, 8, 128, 16, 256, "fixed", (4096,), seqlen_q=8,
         causal=True, description="B=64 Hq=32 Hkv=8 D=128 P=16 L=4096, 8 causal query tokens"),
+    # Small query groups at config 2's bytes: one query head per KV head (MHA) and two.  The
+    # MFMA tiles then hold 1 or 2 live rows of 16.
+    "group1_llama3_8b": DecodeSpec(
+        "group1_llama3_8b", 64, 8, 8, 128, 16, 256, "fixed", (4096,),
+        description="B=64 Hq=8 Hkv=8 (group 1) D=128 P=16 L=4096"),
+    "group2_llama3_8b": DecodeSpec(
+        "group2_llama3_8b", 64, 16, 8, 128, 16, 256, "fixed", (4096,),
+        description="B=64 Hq=16 Hkv=8 (group 2) D=128 P=16 L=4096"),
 }
 
 # The reference's case table: case -> (batch, seqlen_k capacity, num_heads_k)

@@ -65,6 +65,37 @@ def test_append_skips_and_flags_overflow_and_bad_pages():
     assert read_device_status(ws) == _lib.MX_DEVICE_SEQ_TOO_LONG | _lib.MX_DEVICE_BAD_PAGE_ID
 
 
+@pytest.mark.parametrize("entry", ["append", "append_fp8", "attend_one_launch",
+                                   "attend_two_launches"])
+def test_lengths_near_int32_max_flag_and_write_nothing(entry):
+    """seq_lens close to 2^31 - 1: max(L, 0) + j must not wrap to a negative position that
+    passes the table-row check.  Every new token is flagged as past its row, the pools stay
+    byte-identical (the oracle agrees), and nothing outside them is read or written."""
+    from mx_flash_attn_kernel_opt__amd import paged_gqa_decode_append
+    P, Hkv, D = 16, 8, 128
+    S = 17 if entry == "attend_two_launches" else 4
+    k, v, table, g = _pools(2, 4, P, Hkv, D, seed=8)      # 64 slots per row
+    kn = torch.randn(2, S, Hkv, D, generator=g).to(torch.bfloat16)
+    vn = torch.randn(2, S, Hkv, D, generator=g).to(torch.bfloat16)
+    lens_t = torch.tensor([2**31 - 2, 2**31 - 1 - S // 2], dtype=torch.int32)
+    k2, v2, flags = paged_kv_append_reference(kn, vn, k, v, table, lens_t)
+    assert flags == {"seq_too_long"} and torch.equal(k2, k) and torch.equal(v2, v)
+    if entry == "append_fp8":
+        k, v = k.to(torch.float8_e4m3fn), v.to(torch.float8_e4m3fn)
+    kd, vd, td, ld = k.to(DEV), v.to(DEV), table.to(DEV), lens_t.to(DEV)
+    ws = make_workspace(1 << 20, DEV)
+    print(entry, flush=True)
+    if entry.startswith("append"):
+        paged_kv_append(kn.to(DEV), vn.to(DEV), kd, vd, td, ld, workspace=ws)
+    else:
+        q = torch.randn(2, Hkv * 4, D, generator=g).to(torch.bfloat16)
+        paged_gqa_decode_append(q.to(DEV), kn.to(DEV), vn.to(DEV), kd, vd, td, ld, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(kd.cpu().view(torch.uint8), k.view(torch.uint8))
+    assert torch.equal(vd.cpu().view(torch.uint8), v.view(torch.uint8))
+    assert read_device_status(ws) == _lib.MX_DEVICE_SEQ_TOO_LONG
+
+
 @pytest.mark.parametrize("ns", [0, 1, -5])
 def test_append_then_decode(ns):
     """One decode step as a serving loop runs it: append the new token, then attend over
@@ -108,7 +139,7 @@ def test_append_and_attend_matches_the_oracle(S, sq, causal, ns):
     """One call appends the S new tokens and decodes the sq query tokens over L + S keys;
     the pools are bit-exact against the oracle's append, the output within tolerance.  S <= 16
     runs as one launch (the new keys are an extra chunk of each unit), S = 17 as the append
-    kernel followed by the decode; ns 20 takes the split grid's separate combine kernel."""
+    kernel followed by the decode; ns 20 takes the split grid's two-level in-kernel tree."""
     from mx_flash_attn_kernel_opt__amd import paged_gqa_decode_append
     from oracle import paged_decode_append_reference
     lens = [0, 1, 15, 16, 100, 1000, 2047, -3]

@@ -35,16 +35,23 @@ def _workspace(inp, num_splits):
     return make_workspace(p["workspace_bytes"], DEV), p
 
 
+MANY_UNITS = [40 + (b % 7) for b in range(1600)]   # 12 800 units: more than the counters
+
+
 @pytest.mark.parametrize("num_splits,schedule,launches", [
     (0, "balanced", 1),      # merge tree with arrival counters reset in-kernel
-    (4, "split_grid", 1),    # last split merges (arrival counter reset by it)
-    (32, "split_grid", 2),   # split kernel + combine kernel
+    (4, "split_grid", 1),    # one-level split tree (arrival counters reset by it)
+    (32, "split_grid", 1),   # two-level split tree
     (1, "split_grid", 1),
+    (2, "split_grid", 2),    # on MANY_UNITS: split kernel + combine kernel
 ])
 @pytest.mark.parametrize("sq,causal", [(1, False), (4, True)])
 def test_captured_decode_replays_to_the_eager_result(num_splits, schedule, launches, sq, causal):
     lens = [1, 17, 300, 2500, 4096, 0, 999] + [1500] * 9
-    inp = _inputs(lens, 32, 8, 128, 16, sq=sq, seed=num_splits + sq)
+    Hq, Hkv, D = 32, 8, 128
+    if launches == 2:
+        lens, Hq, D = MANY_UNITS, 16, 64
+    inp = _inputs(lens, Hq, Hkv, D, 16, sq=sq, seed=num_splits + sq)
     ws, p = _workspace(inp, num_splits)
     assert p["schedule"] == schedule and p["launches"] == launches
     out = torch.empty_like(inp.q)

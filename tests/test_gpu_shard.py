@@ -95,8 +95,8 @@ def _ragged(B, lo, hi, seed):
     (0, "balanced"),        # automatic: 128 units -> balanced; long units -> merge tree
     (1, "split_grid"),      # one split per sequence: the main kernel writes the rows
     (4, "split_grid"),      # in-kernel merge by the last split (one shard: up to 4 splits)
-    (32, "split_grid"),     # one shard: 32 splits, the combine kernel writes the rows; four
-                            # shards: up to 8 splits of a quarter sequence, merged in-kernel
+    (32, "split_grid"),     # one shard: 32 splits, a two-level in-kernel tree writes the rows;
+                            # four shards: up to 8 splits of a quarter sequence
 ])
 def test_shards_merge_to_the_unsharded_decode(num_splits, expect, num_shards):
     lens = [0, 1, 15, 16, 17] + _ragged(11, 100, 3000, seed=1)

@@ -307,17 +307,24 @@ def test_append_of_zero_tokens_is_a_no_op():
 
 
 def test_python_launch_count_mirrors_the_library_constants():
-    """decode.plan()'s "launches" mirrors kFusedMaxSplits / kMaxSlots of the kernel source."""
+    """decode.plan()'s "launches" mirrors kSplitFanIn / kMaxSlots of the kernel source."""
     import re
     from mx_flash_attn_kernel_opt__amd import decode
     src = open(os.path.join(REPO, "mx_flash_attn_kernel_opt__amd", "csrc",
                             "paged_decode.hip")).read()
-    assert int(re.search(r"kFusedMaxSplits = (\d+);", src).group(1)) == decode.FUSED_MAX_SPLITS
+    assert int(re.search(r"kSplitFanIn = (\d+);", src).group(1)) == decode.SPLIT_FAN_IN
     m = re.search(r"kMaxSlots = (\d+) \+ (\d+);", src)
     assert int(m.group(1)) + int(m.group(2)) == decode.COUNTER_SLOTS
     assert plan(4, 32, 8, 128, 16, 64, 0, 4, num_cus=256)["launches"] == 1
-    assert plan(4, 32, 8, 128, 16, 64, 0, 32, num_cus=256)["launches"] == 2
+    assert plan(4, 32, 8, 128, 16, 64, 0, 32, num_cus=256)["launches"] == 1    # two-level tree
+    assert plan(4, 32, 8, 128, 16, 4096, 0, 4096, num_cus=256)["launches"] == 1
+    # 512 sequences x 8 KV heads x 4 counter groups (64 splits) exceed the 12 288 counters
+    assert plan(512, 32, 8, 128, 16, 64, 0, 64, num_cus=256)["launches"] == 2
+    assert plan(384, 32, 8, 128, 16, 64, 0, 64, num_cus=256)["launches"] == 1
     assert plan(64, 32, 8, 128, 16, 64, 0, 0, num_cus=256)["launches"] == 1   # balanced
+    # the long-context configurations are one launch
+    for B, L in ((1, 32768), (1, 131072), (4, 32768), (4, 131072)):
+        assert plan(B, 64, 8, 128, 16, L // 16, 0, 0, num_cus=256)["launches"] == 1
 
 
 @pytest.mark.parametrize("B,SQ,Hq,Hkv,ns,paired", [
