@@ -133,6 +133,30 @@ int mx_paged_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
                         int32_t phase, void* stream);
 
 /*
+ * mx_paged_gqa_decode for callers that cannot allocate device memory: code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  No counterpart in the
+ * reference.  Arguments as mx_paged_gqa_decode (phase 0), without a workspace: the call uses a
+ * library-owned device array of MX_NOALLOC_SCRATCH_BYTES per GPU, which the HIP runtime places
+ * on each device when the library's code is first loaded there and holds until the process
+ * ends.  The call never allocates (no hipMalloc, hipFree or allocating library routine); the
+ * first call on a device also launches a clear of the array's status word and counters on
+ * `stream`, ahead of its decode.  A call whose mx_paged_gqa_decode_workspace_size exceeds
+ * MX_NOALLOC_SCRATCH_BYTES is rejected with MX_STATUS_UNSUPPORTED before anything is launched.
+ * Every such call on one GPU shares that GPU's array: calls that overlap in time on one GPU
+ * (different streams without ordering, or different host threads) race on it, so order them
+ * on one stream.  The device status flags of these calls are kept in the array and are not
+ * reported through mx_read_device_status.  Returns MX_STATUS_*.
+ */
+#define MX_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
+int mx_paged_gqa_decode_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                void* out, const int32_t* seq_lens, const int32_t* block_table,
+                                int64_t batch, int64_t seqlen_q, int64_t num_heads,
+                                int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                                int64_t num_pages, int64_t max_pages_per_seq,
+                                int64_t max_seq_len, int32_t causal, float scale,
+                                int64_t num_splits, void* stream);
+
+/*
  * The decode over an fp8 K/V cache: k_cache and v_cache hold OCP e4m3fn bytes (torch
  * float8_e4m3fn) in the same [num_pages, page_size, num_kv_heads, head_dim] layout, and the
  * keys and values are k_scale and v_scale times the stored values (per-tensor scales, as in

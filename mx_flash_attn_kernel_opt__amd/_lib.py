@@ -55,6 +55,10 @@ SIGNATURES = {
         ctypes.c_int,
         [_VP] * 6 + [_I64] * 9 + [_I32, _F32, _I64, _VP, _I64, _I32, _VP],
     ),
+    "mx_paged_gqa_decode_noalloc": (
+        ctypes.c_int,
+        [_VP] * 6 + [_I64] * 9 + [_I32, _F32, _I64, _VP],
+    ),
     "mx_paged_gqa_decode_fp8kv": (
         ctypes.c_int,
         [_VP] * 6 + [_I64] * 9 + [_I32, _F32, _F32, _F32, _I64, _VP, _I64, _I32, _VP],

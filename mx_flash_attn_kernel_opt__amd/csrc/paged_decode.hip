@@ -2676,6 +2676,67 @@ int launch_append(const void* k_new, const void* v_new, void* k_cache, void* v_c
   return ok();
 }
 
+// ------------------------------------------------------------------------------------------
+// Workspace of the allocation-free entry point (mx_paged_gqa_decode_noalloc)
+// ------------------------------------------------------------------------------------------
+
+// Clears n words at p (a kernel rather than hipMemsetAsync, which a stream capture would record
+// as a memset node).
+__global__ __launch_bounds__(256) void mx_zero_words(uint32_t* __restrict__ p, int n) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0u;
+}
+
+}  // namespace
+
+// The workspace of every mx_paged_gqa_decode_noalloc call on a device: a file-scope device array
+// that the HIP runtime places on each device when the library's code is loaded there, held until
+// the process ends.  Host code never uses this name as an address (on the host it is only a
+// stand-in): scratch_address() looks up each device's own copy.
+static __device__ __align__(256) char scratch[MX_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+struct ScratchState {
+  void* ptr = nullptr;  // this device's copy of `scratch`
+  bool cleared = false;  // status word and merge counters zeroed by a launch on some stream
+};
+std::mutex g_scratch_mu;
+std::vector<ScratchState> g_scratch;
+
+// This device's copy of `scratch`, found with hipGetSymbolAddress on the device's first call.
+// The first call also launches a clear of the status word and the merge counters on `stream`,
+// ahead of its decode (the kernels leave the counters at zero after every call).
+int scratch_address(hipStream_t stream, void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(MX_STATUS_HIP_ERROR, "hipGetDevice failed");
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if ((int)g_scratch.size() <= dev) g_scratch.resize(dev + 1);
+  ScratchState& sc = g_scratch[dev];
+  if (sc.ptr == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();
+      return fail(MX_STATUS_HIP_ERROR, "hipGetSymbolAddress of the no-alloc scratch failed");
+    }
+    sc.ptr = p;
+  }
+  if (!sc.cleared) {
+    constexpr int kWords = (int)(kPartialBase / 4);
+    hipLaunchKernelGGL(mx_zero_words, dim3((kWords + 255) / 256), dim3(256), 0, stream,
+                       static_cast<uint32_t*>(sc.ptr), kWords);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+      return fail(MX_STATUS_HIP_ERROR, std::string("clearing the no-alloc scratch failed: ") +
+                                           hipGetErrorString(e));
+    sc.cleared = true;
+  }
+  *out = sc.ptr;
+  return MX_STATUS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -2694,6 +2755,36 @@ int mx_paged_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
                      seqlen_q, num_heads, num_kv_heads, head_dim, page_size, num_pages,
                      max_pages_per_seq, max_seq_len, causal, scale, num_splits, workspace,
                      workspace_bytes, phase, stream);
+}
+
+int mx_paged_gqa_decode_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                void* out, const int32_t* seq_lens, const int32_t* block_table,
+                                int64_t batch, int64_t seqlen_q, int64_t num_heads,
+                                int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                                int64_t num_pages, int64_t max_pages_per_seq,
+                                int64_t max_seq_len, int32_t causal, float scale,
+                                int64_t num_splits, void* stream) {
+  if (!q || !k_cache || !v_cache || !out || !seq_lens || !block_table)
+    return fail(MX_STATUS_NULL_POINTER,
+                "q, k_cache, v_cache, out, seq_lens and block_table must be non-NULL");
+  // The size check comes first, so a call that cannot run changes nothing on the device.
+  const int64_t need = mx_paged_gqa_decode_workspace_size(
+      batch, seqlen_q, num_heads, num_kv_heads, head_dim, page_size, max_pages_per_seq,
+      max_seq_len, num_splits);
+  if (need < 0) return (int)need;
+  if (need > MX_NOALLOC_SCRATCH_BYTES)
+    return fail(MX_STATUS_UNSUPPORTED,
+                "this call needs " + std::to_string(need) +
+                    " bytes of workspace, more than the no-alloc scratch holds (" +
+                    std::to_string((int64_t)MX_NOALLOC_SCRATCH_BYTES) +
+                    "): call mx_paged_gqa_decode with a workspace instead");
+  void* ws = nullptr;
+  const int st = scratch_address(static_cast<hipStream_t>(stream), &ws);
+  if (st != MX_STATUS_OK) return st;
+  return decode_impl(q, k_cache, v_cache, out, nullptr, nullptr, seq_lens, block_table, batch,
+                     seqlen_q, num_heads, num_kv_heads, head_dim, page_size, num_pages,
+                     max_pages_per_seq, max_seq_len, causal, scale, num_splits, ws,
+                     MX_NOALLOC_SCRATCH_BYTES, 0, stream);
 }
 
 int mx_paged_gqa_decode_fp8kv(const void* q, const void* k_cache, const void* v_cache,
