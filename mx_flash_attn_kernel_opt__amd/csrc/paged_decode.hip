@@ -2058,9 +2058,13 @@ bool split_tree_fits(int64_t units, int64_t splits) {
   return units * ceil_div(splits, kSplitFanIn) <= kMaxSlots;
 }
 
-// Balanced schedule: chunk positions charged per unit on top of its chunks, for its query load
-// and pipeline fill (2 -> 6 took ragged decode from 115 to 84 us; 8-16 moved it by < 1 %).
-constexpr int kUnitOverhead = 6;
+// Balanced schedule: chunk positions charged per unit on top of its chunks, for its query load,
+// pipeline fill and merge.  A per-workgroup timeline of ragged decode puts a piece at 0.26 us per
+// chunk plus 2.3 us (1.5 us more when the unit is cut and merged): at 6 positions the units were
+// undercharged, and the workgroups holding many one-chunk units ended last (84 us against a
+// median of 68).  8 took ragged decode from 85.0 to 80.0 us (10 and 12: 81.1, 82.8), the other
+// configurations unchanged.
+constexpr int kUnitOverhead = 8;
 // Balanced schedule limits: the largest batch whose seq_lens scan stays within two passes of
 // one workgroup.
 constexpr int64_t kBalancedMaxBatch = 512;
