@@ -474,6 +474,7 @@ struct MainShape {
   int split_groups;      // split grid: ceil(num_splits / kSplitFanIn), merge counters per unit
   // balanced schedule
   int num_groups;        // workgroups of the launch
+  int chunk_weight;      // balanced schedule: positions per chunk
   int unit_overhead;     // positions charged per (sequence, KV head) on top of its chunks
   int num_slots;         // partial slots: num_groups + batch * Hkv
   // Partial outputs (sharded decode): when o_out is set, each query row is written as its fp32
@@ -1593,6 +1594,7 @@ void mx_paged_decode_balanced(
   // of equal chunks (charging the full overhead to a unit's first piece would leave its other
   // pieces longer, and shares that straddle units would pay two pieces).
   int alpha = sh.unit_overhead;
+  int wc = sh.chunk_weight;
   const int units = B * UPS;
   // (k = 1 needs no change: every workgroup then holds one whole unit whatever the charge.)
   if (sh.num_groups > units && sh.num_groups % units == 0) {  // the same in every thread
@@ -1617,13 +1619,14 @@ void mx_paged_decode_balanced(
     nb_hi = __builtin_amdgcn_readfirstlane(nb_hi);
     if (nb_lo == nb_hi && nb_lo > 0) {
       const int k = sh.num_groups / units;
+      wc = 1;
       alpha = (k - nb_lo % k) % k;
     }
   }
   int mine = 0;
 #pragma unroll
   for (int i = 0; i < kScanPerThread; ++i) {
-    wts[i] = wts[i] > 0 ? UPS * (wts[i] + alpha) : 0;
+    wts[i] = wts[i] > 0 ? UPS * (wts[i] * wc + alpha) : 0;
     mine += wts[i];
   }
   // Total positions of the batch.
@@ -1640,7 +1643,8 @@ void mx_paged_decode_balanced(
 #pragma unroll
   for (int w2 = 0; w2 < NW; ++w2) total += s_int[w2];
   if (total == 0) return;
-  const int qsz = (total + sh.num_groups - 1) / sh.num_groups;
+  // (Shares of at least one chunk's weight: every workgroup a unit spans then holds a chunk.)
+  const int qsz = max((total + sh.num_groups - 1) / sh.num_groups, wc);
   const int x_begin = wg * qsz;
   if (x_begin >= total) return;
   const int x_end = min(x_begin + qsz, total);
@@ -1682,16 +1686,17 @@ void mx_paged_decode_balanced(
 
   SeqExtent ext = seq_extent<kAppend>(seq_lens, b, sh, status, false);
   int n_b = (ext.sched + kChunk - 1) / kChunk;
-  int span = n_b + alpha;
+  int span = n_b * wc + alpha;
   int j = (x_begin - seq_start) / span;  // (KV head, row group) of the unit
   int u0 = seq_start + j * span;  // first position of unit (b, j)
   bool bad_page = false;
 
   for (;;) {
-    // Unit (b, j): positions [u0, u0 + span), its chunk c at position u0 + alpha + c.
+    // Unit (b, j): positions [u0, u0 + span), its chunk c at positions u0 + alpha + c * wc ..;
+    // this workgroup takes the chunks that start in [x_begin, x_end).
     const int cpos = u0 + alpha;
-    const int ca = max(x_begin, cpos) - cpos;
-    const int cb = min(x_end, cpos + n_b) - cpos;
+    const int ca = min(n_b, (max(0, x_begin - cpos) + wc - 1) / wc);
+    const int cb = min(n_b, (max(0, x_end - cpos) + wc - 1) / wc);
     if (ca < cb) {
       const int unit = b * UPS + j;
       const int kv = sh.row_tiles == 1 ? j : j / sh.row_tiles;
@@ -1700,7 +1705,7 @@ void mx_paged_decode_balanced(
       const int nrows = min(16 * KT, sh.rows - r0);
       const int64_t rbase = row_base(b, kv, sh);
       const int first_wg = cpos / qsz;
-      const int npieces = (cpos + n_b - 1) / qsz - first_wg + 1;
+      const int npieces = (cpos + (n_b - 1) * wc) / qsz - first_wg + 1;
       const int n_cache = (ext.cache + kChunk - 1) / kChunk;  // chunks read from the cache
       const int c_mask = kCausal ? min(n_cache - 1, max(0, row_key_limit(r0, ext.keys, sh)) / kChunk)
                                  : n_cache - 1;
@@ -1766,7 +1771,7 @@ void mx_paged_decode_balanced(
       while (ext.sched <= 0 && ++b < B) ext = seq_extent<kAppend>(seq_lens, b, sh, status, false);
       if (b >= B) break;  // unreachable: positions only exist for non-empty sequences
       n_b = (ext.sched + kChunk - 1) / kChunk;
-      span = n_b + alpha;
+      span = n_b * wc + alpha;
     }
   }
   if (bad_page && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
@@ -2064,7 +2069,8 @@ bool split_tree_fits(int64_t units, int64_t splits) {
 // undercharged, and the workgroups holding many one-chunk units ended last (84 us against a
 // median of 68).  8 took ragged decode from 85.0 to 80.0 us (10 and 12: 81.1, 82.8), the other
 // configurations unchanged.
-constexpr int kUnitOverhead = 8;
+constexpr int kChunkPositions = 8;
+constexpr int kUnitOverhead = 8 * kChunkPositions;
 // Balanced schedule limits: the largest batch whose seq_lens scan stays within two passes of
 // one workgroup.
 constexpr int64_t kBalancedMaxBatch = 512;
@@ -2193,7 +2199,8 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
   plan->chunk_shift = shift;
   const int64_t units = batch * num_kv_heads * row_tiles;
   const bool balanced_ok = batch <= kBalancedMaxBatch && units <= kBalancedMaxUnits &&
-                           units * (ceil_div(cap, kChunk) + kUnitOverhead) < kBalancedMaxLine;
+                           units * (ceil_div(cap, kChunk) * kChunkPositions + kUnitOverhead) <
+                               kBalancedMaxLine;
   // Short capacities favour one split per unit (no length scan, no merge): the balanced
   // schedule pays off from 2 048 tokens, or from 1 024 with at least 512 units.
   const bool long_enough = cap >= kBalancedMinCap || (cap >= kBalancedMinCap / 2 && units >= 512);
@@ -2377,6 +2384,7 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   sh.split_groups = 1;
   sh.tokens_per_split = (int)plan.tokens_per_split;
   sh.num_groups = (int)plan.groups;
+  sh.chunk_weight = kChunkPositions;
   sh.unit_overhead = kUnitOverhead;
   sh.num_slots = (int)plan.slots;
   sh.o_out = o_out;
