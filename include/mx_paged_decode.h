@@ -57,9 +57,9 @@ extern "C" {
 /* Schedules reported by mx_paged_gqa_decode_plan. */
 #define MX_SCHEDULE_SPLIT_GRID 0   /* grid (Hkv * row groups, batch, splits); the splits of
                                       each unit merge through an in-kernel tree of arrival
-                                      counters, or, when batch * Hkv * row groups *
-                                      ceil(splits / 16) > 12288, in a combine kernel that
-                                      follows                                                     */
+                                      counters, or, when splits > 4096 or batch * Hkv * row
+                                      groups * ceil(splits / 8) > 12288, in a combine kernel
+                                      that follows                                                */
 #define MX_SCHEDULE_BALANCED 1     /* one launch of a fixed number of workgroups that divide the
                                       batch's K/V chunks evenly from seq_lens on the device and
                                       merge split sequences themselves                            */

@@ -23,7 +23,7 @@
 //    exact.  Masked chunks (sequence tail, causal limits) use selects, never arithmetic on
 //    unused page slots.
 //  * Two schedules, both one launch: the split grid (Hkv * row groups, batch, splits), whose
-//    splits merge their partials through an in-kernel tree of arrival counters (fan-in 16; a
+//    splits merge their partials through an in-kernel tree of arrival counters (fan-in 8; a
 //    combine kernel in a second launch only when the counters do not fit), and a
 //    length-balanced launch that cuts the batch's chunk line into equal shares on the device
 //    and merges cut units through a fan-in-8 tree of the same kind.
@@ -471,7 +471,7 @@ struct MainShape {
   int num_splits;
   int tokens_per_split;  // multiple of page_size
   int fused_combine;     // split grid: the splits of each unit merge their partials in-kernel
-  int split_groups;      // split grid: ceil(num_splits / kSplitFanIn), merge counters per unit
+  int split_groups;      // split grid: ceil(num_splits / kMergeFanIn), merge counters per unit
   // balanced schedule
   int num_groups;        // workgroups of the launch
   int chunk_weight;      // balanced schedule: positions per chunk
@@ -1175,10 +1175,12 @@ __device__ __forceinline__ void copy_new_tokens(const int32_t* __restrict__ seq_
     atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
 }
 
-// Partials merged per step of a cross-workgroup merge tree: the balanced schedule's pieces, and
-// the split grid's splits.
-constexpr int kPieceFanIn = 8;
-constexpr int kSplitFanIn = 16;
+// Partials merged per step of a cross-workgroup merge tree (the balanced schedule's pieces, the
+// split grid's splits); kCounterLevels levels cover 8^4 = 4096 items.  For the split grid 8
+// matched the two-launch combine on long-context decode in interleaved A/B (B=1, 32K: 30.0
+// against 30.0 us), where groups of 16 ran 30.7 and of 4 ran 31.3.
+constexpr int kMergeFanIn = 8;
+constexpr int kMaxMergeItems = 8 * 8 * 8 * 8;
 
 // Cross-workgroup handoff of partials (the split grid's in-kernel merge and the balanced
 // kernel's merge tree).  Partials are stored and loaded with relaxed agent-scope atomic
@@ -1343,7 +1345,7 @@ __device__ __forceinline__ void merge_tree(const Tree& tree, int item, int nitem
 // The split grid's merge tree over the splits of one unit (merge_tree).  Partials are row-major
 // over the query rows with the splits innermost: part_o[(row * num_splits + split) * D + d],
 // part_lse[row * num_splits + split] (the layout mx_paged_decode_combine reads).  Each level of
-// the counter region holds split_groups = ceil(num_splits / kSplitFanIn) counters per unit.
+// the counter region holds split_groups = ceil(num_splits / kMergeFanIn) counters per unit.
 template <int D>
 struct SplitTree {
   const MainShape& sh;
@@ -1363,7 +1365,7 @@ struct SplitTree {
   }
   __device__ __forceinline__ uint32_t* counter(int level, int slot) const {
     return counters + (int64_t)level * kMaxSlots + (int64_t)unit * sh.split_groups +
-           slot / kSplitFanIn;
+           slot / kMergeFanIn;
   }
   __device__ __forceinline__ void store(int hh, int d, f32x4 v, float l) const {
     store_row4<D>(out, sh, row(hh), d, v, l);
@@ -1384,7 +1386,7 @@ struct SplitTree {
 //
 // A sequence cut into several splits leaves one normalised partial (O/l, log2-sum-exp) per
 // split and row.  With fused_combine the splits of each unit merge them through an in-kernel
-// tree (merge_tree: groups of kSplitFanIn splits, the last arrival of a group merges it), so the
+// tree (merge_tree: groups of kMergeFanIn splits, the last arrival of a group merges it), so the
 // whole call is one launch; otherwise mx_paged_decode_combine merges them in a second launch.
 template <int D, int NBUF, int NW, bool kCausal, int KT, bool kAppend, bool kFp8>
 __global__ __launch_bounds__(64 * NW)
@@ -1492,7 +1494,7 @@ void mx_paged_decode_splitkv(
   const int nsv = (seq + sh.tokens_per_split - 1) / sh.tokens_per_split;  // splits with tokens
   const SplitTree<D> tree{sh,  part_o, part_lse, counters, out, row_base(b, kv, sh), r0,
                           b * (int)gridDim.x + (int)blockIdx.x};
-  merge_tree<D, NW, kSplitFanIn>(tree, split, nsv, nrows, s_lse, &s_last);
+  merge_tree<D, NW, kMergeFanIn>(tree, split, nsv, nrows, s_lse, &s_last);
   copy_if_writer();
 }
 
@@ -1756,7 +1758,7 @@ void mx_paged_decode_balanced(
           }
         }
         const BalancedTree<D> tree{sh, part_o, part_lse, counters, out, rbase, r0, slot0, TR};
-        merge_tree<D, NW, kPieceFanIn>(tree, item, npieces, nrows, s_lse, &s_int[NW + 2]);
+        merge_tree<D, NW, kMergeFanIn>(tree, item, npieces, nrows, s_lse, &s_int[NW + 2]);
       }
       // The merged states in LDS share bytes with the K tiles the next piece streams into:
       // no wave may start that piece until every wave has finished reading them.
@@ -2057,10 +2059,10 @@ constexpr int64_t kMaxMergeRows = int64_t(1) << 25;  // mx_lse_merge: 64 * rows 
 int64_t groups_per_cu(int64_t head_dim) { return head_dim == 64 ? 2 : 1; }
 
 // Whether the split grid's units merge their splits in-kernel (one launch): each level of the
-// counter region must hold ceil(splits / kSplitFanIn) counters per unit.  Otherwise the combine
-// kernel merges in a second launch.
+// counter region must hold ceil(splits / kMergeFanIn) counters per unit, and the tree's levels
+// cover at most kMaxMergeItems splits.  Otherwise the combine kernel merges in a second launch.
 bool split_tree_fits(int64_t units, int64_t splits) {
-  return units * ceil_div(splits, kSplitFanIn) <= kMaxSlots;
+  return splits <= kMaxMergeItems && units * ceil_div(splits, kMergeFanIn) <= kMaxSlots;
 }
 
 // Balanced schedule: chunk positions charged per unit on top of its chunks, for its query load,
@@ -2431,7 +2433,7 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   // counters fit the counter region and the caller did not ask for the two phases separately.
   const bool fused = phase == 0 && plan.splits > 1 &&
                      split_tree_fits(batch * num_kv_heads * plan.row_tiles, plan.splits);
-  sh.split_groups = (int)ceil_div(plan.splits, kSplitFanIn);
+  sh.split_groups = (int)ceil_div(plan.splits, kMergeFanIn);
   sh.fused_combine = fused ? 1 : 0;
   if (phase != MX_PHASE_COMBINE_ONLY) {
     const dim3 grid((unsigned)(num_kv_heads * plan.row_tiles), (unsigned)batch,

@@ -17,7 +17,8 @@ import torch
 from . import _lib
 
 
-SPLIT_FAN_IN = 16            # kSplitFanIn in csrc/paged_decode.hip
+MERGE_FAN_IN = 8             # kMergeFanIn in csrc/paged_decode.hip
+MAX_MERGE_ITEMS = 8 ** 4     # kMaxMergeItems
 COUNTER_SLOTS = 4096 + 8192  # kMaxSlots in csrc/paged_decode.hip
 
 
@@ -55,13 +56,14 @@ def plan(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, page_size
     _lib.check(st)
     schedule = "balanced" if sch.value == _lib.MX_SCHEDULE_BALANCED else "split_grid"
     # Launches of a phase-0 call: the balanced schedule and the split grid with one split are
-    # one launch; the split grid merges its splits through an in-kernel tree when every unit's
-    # ceil(splits / SPLIT_FAN_IN) arrival counters fit the counter region, else a combine
-    # kernel follows (csrc/paged_decode.hip, split_tree_fits).  The split grid launches
-    # units x splits workgroups.
+    # one launch; the split grid merges its splits through an in-kernel tree when there are at
+    # most MAX_MERGE_ITEMS and every unit's ceil(splits / MERGE_FAN_IN) arrival counters fit the
+    # counter region, else a combine kernel follows (csrc/paged_decode.hip, split_tree_fits).
+    # The split grid launches units x splits workgroups.
     units = wgs.value // max(ns.value, 1)
     two = (schedule == "split_grid" and ns.value > 1 and
-           units * math.ceil(ns.value / SPLIT_FAN_IN) > COUNTER_SLOTS)
+           (ns.value > MAX_MERGE_ITEMS or
+            units * math.ceil(ns.value / MERGE_FAN_IN) > COUNTER_SLOTS))
     return {"schedule": schedule, "splits": ns.value, "tokens_per_split": tps.value,
             "workgroups": wgs.value, "workspace_bytes": ws.value, "launches": 2 if two else 1}
 

@@ -523,10 +523,10 @@ def test_split_grid_fused_merge_matches_two_phase_combine():
     assert torch.equal(again, fused)
 
 
-@pytest.mark.parametrize("ns", [17, 32, 33, 64, 255, 300])
+@pytest.mark.parametrize("ns", [8, 9, 32, 64, 65, 255, 300])
 def test_split_grid_merge_tree_levels(ns):
-    """Split counts across the in-kernel tree's levels (groups of 16: one level up to 16
-    splits, two up to 256, three above), against the oracle and the two-phase combine."""
+    """Split counts across the in-kernel tree's levels (groups of 8: one level up to 8 splits,
+    two up to 64, three up to 512), against the oracle and the two-phase combine."""
     from mx_flash_attn_kernel_opt__amd import _lib, make_workspace, plan
 
     lens = [1, 16, 17, 300, 4799, 4800, 2500, 0, 4097]
