@@ -70,9 +70,52 @@ constexpr float kRescaleSlack = 8.0f;  // log2 units the stale running max may l
 // calls left behind.
 constexpr int kStatusBytes = 256;
 constexpr int kMaxSlots = 4096 + 8192;          // balanced: workgroups + batch * Hkv
+constexpr int kBalancedBatch = 512;             // balanced: largest batch
 constexpr int kCounterLevels = 4;               // fan-in-8 merge tree levels
 constexpr int64_t kCounterBytes = (int64_t)kCounterLevels * kMaxSlots * 4;
 constexpr int64_t kPartialBase = kStatusBytes + kCounterBytes;
+
+// ------------------------------------------------------------------------------------------
+// Per-workgroup timeline (profiling builds only)
+// ------------------------------------------------------------------------------------------
+
+// Built with -DMX_WG_TIMELINE (as mx_flash_attn_kernel_opt__amd/timeline.py does), the main
+// kernels record per workgroup (linear id below kTimelineSlots) the wall clock (100 MHz) at
+// entry, at the start of its first streamed piece, at the end of its last one and at exit,
+// plus the XCD it ran on and the number of pieces it streamed; mx_timeline_read copies the
+// table out.  Thread 0 writes its workgroup's row with plain vector stores.  In the default
+// build WgTimeline is an empty struct whose calls compile to nothing.
+#ifdef MX_WG_TIMELINE
+constexpr int kTimelineSlots = 16384;
+constexpr int kTimelineFields = 6;  // entry, first stream begin, last stream end, exit, XCD, pieces
+__device__ unsigned long long g_timeline[kTimelineSlots][kTimelineFields];
+struct WgTimeline {
+  int pieces = 0;
+  __device__ static void put(int field, unsigned long long v) {
+    const int slot = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    if (threadIdx.x == 0 && slot < kTimelineSlots) g_timeline[slot][field] = v;
+  }
+  __device__ WgTimeline() {
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    put(0, wall_clock64());
+    put(4, xcc);
+  }
+  __device__ ~WgTimeline() {
+    put(3, wall_clock64());
+    put(5, (unsigned long long)pieces);
+  }
+  __device__ void stream_begin() {
+    if (pieces++ == 0) put(1, wall_clock64());
+  }
+  __device__ void stream_end() { put(2, wall_clock64()); }
+};
+#else
+struct WgTimeline {
+  __device__ void stream_begin() {}
+  __device__ void stream_end() {}
+};
+#endif
 
 // ------------------------------------------------------------------------------------------
 // Device helpers
@@ -87,6 +130,25 @@ __device__ __forceinline__ float group_max4(float x) {
   x = fmaxf(as_float(a[0]), as_float(a[1]));
   auto b = __builtin_amdgcn_permlane16_swap(as_u32(x), as_u32(x), false, false);
   return fmaxf(as_float(b[0]), as_float(b[1]));
+}
+
+// floor(x / d) for 0 <= x < 2^31, given inv = 1.0 / d (d >= 1): (x + 1/2) / d lies at least
+// 1/(2d) from every integer, while the double product's relative error is below 2^-51, i.e.
+// (x + 1/2) / d * 2^-51 < 1/(2d) for every such x.
+__device__ __forceinline__ int div_floor(int x, double inv) {
+  return (int)(((double)x + 0.5) * inv);
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave (row shifts, then the row broadcasts of
+// lanes 15 and 31), without LDS.
+__device__ __forceinline__ int wave_inclusive_sum(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
+  return x;
 }
 
 __device__ __forceinline__ float group_sum4(float x) {
@@ -512,16 +574,18 @@ __device__ __forceinline__ void scale_o_by_v_scale(SoftmaxState<D> (&st)[KT],
     for (int i = 0; i < D / 16; ++i) st[t].o[i] *= sh.v_scale;
 }
 
-// Keys of sequence b before clamping (see MainShape::appended).
-__device__ __forceinline__ int key_count(const int32_t* seq_lens, int b, int appended) {
-  const int L = seq_lens[b];
+// Keys of a sequence whose seq_lens entry is L, before clamping (see MainShape::appended).
+__device__ __forceinline__ int key_count_of(int L, int appended) {
   return appended > 0 ? keys_after_append(L, appended) : L;
+}
+__device__ __forceinline__ int key_count(const int32_t* seq_lens, int b, int appended) {
+  return key_count_of(seq_lens[b], appended);
 }
 
 // Sequence length as the kernels see it: clamped to the planned capacity (flagged).
-__device__ __forceinline__ int clamped_len(const int32_t* seq_lens, int b, const MainShape& sh,
-                                           uint32_t* status, bool report) {
-  int seq = key_count(seq_lens, b, sh.appended);
+__device__ __forceinline__ int clamped_len_of(int L, const MainShape& sh, uint32_t* status,
+                                              bool report) {
+  int seq = key_count_of(L, sh.appended);
   if (seq > sh.cap_tokens) {
     if (report) atomicOr(status, (uint32_t)MX_DEVICE_SEQ_TOO_LONG);
     seq = sh.cap_tokens;
@@ -870,18 +934,23 @@ struct SeqExtent {
   int at;
 };
 template <bool kAppend>
-__device__ __forceinline__ SeqExtent seq_extent(const int32_t* seq_lens, int b,
-                                                const MainShape& sh, uint32_t* status,
-                                                bool report) {
+__device__ __forceinline__ SeqExtent seq_extent_of(int L, const MainShape& sh, uint32_t* status,
+                                                   bool report) {
   if constexpr (!kAppend) {
-    const int s = clamped_len(seq_lens, b, sh, status, report);
+    const int s = clamped_len_of(L, sh, status, report);
     return SeqExtent{s, s, s, 0};
   }
-  const int at = max(seq_lens[b], 0);
+  const int at = max(L, 0);
   if (at > sh.cap_tokens - sh.new_tokens && report)
     atomicOr(status, (uint32_t)MX_DEVICE_SEQ_TOO_LONG);
   const int c = min(at, sh.cap_tokens);
   return SeqExtent{c + sh.new_tokens, c, max(c, 1), at};
+}
+template <bool kAppend>
+__device__ __forceinline__ SeqExtent seq_extent(const int32_t* seq_lens, int b,
+                                                const MainShape& sh, uint32_t* status,
+                                                bool report) {
+  return seq_extent_of<kAppend>(seq_lens[b], sh, status, report);
 }
 
 // The fused append's extra chunk of unit (b, kv), a stream_chunks hook: in the wave that owns
@@ -1402,6 +1471,7 @@ void mx_paged_decode_splitkv(
   __shared__ __attribute__((aligned(16))) char lds[L::kBytes];
   __shared__ int s_last;
   __shared__ float s_lse[16 * KT];
+  WgTimeline timeline;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   // Wave index, made provably wave-uniform so the chunk indices derived from it stay in
@@ -1452,6 +1522,7 @@ void mx_paged_decode_splitkv(
   bool bad_page = false;
   const int32_t* bt_row = block_table + (int64_t)b * sh.max_pages;
   const int c_end = min(c_hi, n_cache);
+  timeline.stream_begin();
   if constexpr (kAppend) {
     // Fused append: the split holding the last schedule chunk also takes the new keys, as one
     // more chunk after its cache chunks in the waves' round-robin order.
@@ -1466,6 +1537,7 @@ void mx_paged_decode_splitkv(
         st, qop, kc, vc, bt_row, kv, c_lo, c_end, ext.cache, c_mask, row_lim, wv,
         L::ktile(lds, wv), sh, bad_page);
   }
+  timeline.stream_end();
   if constexpr (kFp8) scale_o_by_v_scale<D, KT>(st, sh);
   if (bad_page && lane == 0) atomicOr(status, (uint32_t)MX_DEVICE_BAD_PAGE_ID);
   publish_wave_state<D, NW, KT>(lds, st, wv);
@@ -1555,6 +1627,8 @@ void mx_paged_decode_balanced(
   __shared__ int s_int[NW + 4];
   __shared__ int s_mm[2 * NW];
   __shared__ float s_lse[16 * KT];
+  __shared__ int s_len[kBalancedBatch];  // the batch's seq_lens entries
+  WgTimeline timeline;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1563,27 +1637,20 @@ void mx_paged_decode_balanced(
   const int UPS = sh.num_kv_heads * sh.row_tiles;    // units per sequence
   const int B = sh.batch;
 
-  // Empty sequences (L <= 0) are defined as zero output; sequence b's zeros (its seqlen_q *
-  // num_heads consecutive rows) are written by workgroup b % num_groups.
-  for (int b = wg; b < B; b += sh.num_groups) {
-    if (!kAppend && key_count(seq_lens, b, sh.appended) <= 0) {
-      const int64_t row0 = (int64_t)b * sh.seqlen_q * sh.num_heads;
-      for (int e = tid; e < sh.seqlen_q * sh.num_heads * (D / 4); e += 64 * NW)
-        store_row4<D>(out, sh, row0 + e / (D / 4), 4 * (e % (D / 4)), f32x4{0.f, 0.f, 0.f, 0.f},
-                      -INFINITY);
-    }
-  }
-
-  // Sequence weights (positions per sequence).  The batch is at most 512 sequences, so every
-  // thread reads its few seq_lens once and keeps their weights in registers for both the total
-  // and the scan that locates this workgroup's first position.
-  constexpr int kScanPerThread = (512 + 64 * NW - 1) / (64 * NW);
+  // Sequence weights (positions per sequence).  The batch is at most kBalancedBatch sequences:
+  // thread tid reads the kScanPerThread consecutive entries from b = tid * kScanPerThread on
+  // once and keeps their weights in registers for both the total and the scan that locates
+  // this workgroup's first position.  The entries also go to LDS, where the empty-sequence
+  // check and the unit walk read them.
+  constexpr int kScanPerThread = (kBalancedBatch + 64 * NW - 1) / (64 * NW);
   int wts[kScanPerThread];  // chunks of the sequence, then its positions
   int nb_lo = INT_MAX, nb_hi = 0;
 #pragma unroll
   for (int i = 0; i < kScanPerThread; ++i) {
-    const int b = i * 64 * NW + tid;
-    const int seq = b < B ? seq_extent<kAppend>(seq_lens, b, sh, status, wg == 0).sched : 0;
+    const int b = tid * kScanPerThread + i;
+    const int len = b < B ? seq_lens[b] : 0;
+    if (b < B) s_len[b] = len;
+    const int seq = b < B ? seq_extent_of<kAppend>(len, sh, status, wg == 0).sched : 0;
     wts[i] = seq > 0 ? (seq + kChunk - 1) / kChunk : 0;
     if (b < B) {
       nb_lo = min(nb_lo, wts[i]);
@@ -1631,54 +1698,46 @@ void mx_paged_decode_balanced(
     wts[i] = wts[i] > 0 ? UPS * (wts[i] * wc + alpha) : 0;
     mine += wts[i];
   }
-  // Total positions of the batch.
-  int incl = mine;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(incl, off);
-    if (lane >= off) incl += y;
-  }
+  // One scan over the workgroup: positions before this thread's first sequence, and the total.
+  const int incl = wave_inclusive_sum(mine);
   if (tid == 0) s_int[NW] = -1;
   if (lane == 63) s_int[wv] = incl;
   __syncthreads();
-  int total = 0;
+  // Empty sequences (L <= 0) are defined as zero output; sequence b's zeros (its seqlen_q *
+  // num_heads consecutive rows) are written by workgroup b % num_groups.
+  if constexpr (!kAppend) {
+    for (int b = wg; b < B; b += sh.num_groups) {
+      if (key_count_of(s_len[b], sh.appended) <= 0) {
+        const int64_t row0 = (int64_t)b * sh.seqlen_q * sh.num_heads;
+        for (int e = tid; e < sh.seqlen_q * sh.num_heads * (D / 4); e += 64 * NW)
+          store_row4<D>(out, sh, row0 + e / (D / 4), 4 * (e % (D / 4)),
+                        f32x4{0.f, 0.f, 0.f, 0.f}, -INFINITY);
+      }
+    }
+  }
+  int total = 0, before = 0;
 #pragma unroll
-  for (int w2 = 0; w2 < NW; ++w2) total += s_int[w2];
+  for (int w2 = 0; w2 < NW; ++w2) {
+    total += s_int[w2];
+    before += w2 < wv ? s_int[w2] : 0;
+  }
   if (total == 0) return;
   // (Shares of at least one chunk's weight: every workgroup a unit spans then holds a chunk.)
   const int qsz = max((total + sh.num_groups - 1) / sh.num_groups, wc);
   const int x_begin = wg * qsz;
   if (x_begin >= total) return;
   const int x_end = min(x_begin + qsz, total);
-  // Positions are laid out sequence by sequence: thread tid's i-th sequence b = i*64*NW + tid
-  // starts after all sequences of smaller index, i.e. after blocks < i of every thread plus
-  // the block-i sequences of lower threads.  Blocks are scanned one at a time.
+  // Positions are laid out sequence by sequence, so the sequence holding x_begin is found by
+  // exactly one thread (the positions of non-empty sequences tile [0, total)).
   {
-    int carry = 0;
+    int start = before + incl - mine;
 #pragma unroll
     for (int i = 0; i < kScanPerThread; ++i) {
-      int incl_i = wts[i];
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const int y = __shfl_up(incl_i, off);
-        if (lane >= off) incl_i += y;
-      }
-      __syncthreads();
-      if (lane == 63) s_int[wv] = incl_i;
-      __syncthreads();
-      int blk_before = 0, blk_total = 0;
-#pragma unroll
-      for (int w2 = 0; w2 < NW; ++w2) {
-        blk_before += (w2 < wv) ? s_int[w2] : 0;
-        blk_total += s_int[w2];
-      }
-      const int start = carry + blk_before + incl_i - wts[i];
       if (wts[i] > 0 && start <= x_begin && x_begin < start + wts[i]) {
-        s_int[NW] = i * 64 * NW + tid;
+        s_int[NW] = tid * kScanPerThread + i;
         s_int[NW + 1] = start;
       }
-      carry += blk_total;
-      if (carry > x_begin) break;  // uniform: carry is the same in every thread
+      start += wts[i];
     }
     __syncthreads();
   }
@@ -1686,10 +1745,21 @@ void mx_paged_decode_balanced(
   int seq_start = __builtin_amdgcn_readfirstlane(s_int[NW + 1]);
   if (b < 0) return;  // unreachable: the positions of non-empty sequences tile [0, total)
 
-  SeqExtent ext = seq_extent<kAppend>(seq_lens, b, sh, status, false);
+  // (LDS values are uniform here; readfirstlane keeps the unit walk in scalar registers.)
+  auto extent = [&](int bb) {
+    return seq_extent_of<kAppend>(__builtin_amdgcn_readfirstlane(s_len[bb]), sh, status, false);
+  };
+  SeqExtent ext = extent(b);
   int n_b = (ext.sched + kChunk - 1) / kChunk;
   int span = n_b * wc + alpha;
-  int j = (x_begin - seq_start) / span;  // (KV head, row group) of the unit
+  // The unit walk divides only through shifts (the chunk weight is a power of two) and
+  // div_floor: with one wave per SIMD, every step of an integer division's ~35-instruction
+  // sequence would wait out its full latency, on every piece.
+  const int wshift = __builtin_ctz(wc);
+  const double inv_qsz = 1.0 / qsz;
+  int j = div_floor(x_begin - seq_start, 1.0 / span);  // (KV head, row group) of the unit
+  int kv = sh.row_tiles == 1 ? j : j / sh.row_tiles;
+  int grp = j - kv * sh.row_tiles;  // row group: rows grp*16*KT ..
   int u0 = seq_start + j * span;  // first position of unit (b, j)
   bool bad_page = false;
 
@@ -1697,17 +1767,18 @@ void mx_paged_decode_balanced(
     // Unit (b, j): positions [u0, u0 + span), its chunk c at positions u0 + alpha + c * wc ..;
     // this workgroup takes the chunks that start in [x_begin, x_end).
     const int cpos = u0 + alpha;
-    const int ca = min(n_b, (max(0, x_begin - cpos) + wc - 1) / wc);
-    const int cb = min(n_b, (max(0, x_end - cpos) + wc - 1) / wc);
+    const int ca = min(n_b, (max(0, x_begin - cpos) + wc - 1) >> wshift);
+    const int cb = min(n_b, (max(0, x_end - cpos) + wc - 1) >> wshift);
     if (ca < cb) {
       const int unit = b * UPS + j;
-      const int kv = sh.row_tiles == 1 ? j : j / sh.row_tiles;
-      const int grp = j - kv * sh.row_tiles;  // row group: rows grp*16*KT ..
       const int r0 = grp * 16 * KT;
       const int nrows = min(16 * KT, sh.rows - r0);
       const int64_t rbase = row_base(b, kv, sh);
-      const int first_wg = cpos / qsz;
-      const int npieces = (cpos + (n_b - 1) * wc) / qsz - first_wg + 1;
+      // Workgroups holding the unit's first and last chunks: this one when that chunk starts
+      // in [x_begin, x_end) (one does, as ca < cb).
+      const int last = cpos + (n_b - 1) * wc;
+      const int first_wg = cpos >= x_begin ? wg : div_floor(cpos, inv_qsz);
+      const int npieces = (last < x_end ? wg : div_floor(last, inv_qsz)) - first_wg + 1;
       const int n_cache = (ext.cache + kChunk - 1) / kChunk;  // chunks read from the cache
       const int c_mask = kCausal ? min(n_cache - 1, max(0, row_key_limit(r0, ext.keys, sh)) / kChunk)
                                  : n_cache - 1;
@@ -1718,6 +1789,7 @@ void mx_paged_decode_balanced(
       setup_row_group<D, KT>(qop, st, row_lim, q, b, kv, grp, ext.keys, sh, lane);
       const int32_t* bt_row = block_table + (int64_t)b * sh.max_pages;
       const int c_end = min(cb, n_cache);
+      timeline.stream_begin();
       if constexpr (kAppend) {
         // Fused append: the piece holding the unit's last schedule chunk also takes the new
         // keys, as one more chunk after its cache chunks in the waves' round-robin order.
@@ -1731,6 +1803,7 @@ void mx_paged_decode_balanced(
             st, qop, kc, vc, bt_row, kv, ca, c_end, ext.cache, c_mask, row_lim, wv,
             L::ktile(lds, wv), sh, bad_page);
       }
+      timeline.stream_end();
       if constexpr (kFp8) scale_o_by_v_scale<D, KT>(st, sh);
       publish_wave_state<D, NW, KT>(lds, st, wv);
 
@@ -1767,10 +1840,15 @@ void mx_paged_decode_balanced(
     // Next unit.
     u0 += span;
     if (u0 >= x_end) break;
+    if (++grp == sh.row_tiles) {
+      grp = 0;
+      ++kv;
+    }
     if (++j == UPS) {
       j = 0;
+      kv = 0;
       ext.sched = 0;
-      while (ext.sched <= 0 && ++b < B) ext = seq_extent<kAppend>(seq_lens, b, sh, status, false);
+      while (ext.sched <= 0 && ++b < B) ext = extent(b);
       if (b >= B) break;  // unreachable: positions only exist for non-empty sequences
       n_b = (ext.sched + kChunk - 1) / kChunk;
       span = n_b * wc + alpha;
@@ -2071,11 +2149,21 @@ bool split_tree_fits(int64_t units, int64_t splits) {
 // undercharged, and the workgroups holding many one-chunk units ended last (84 us against a
 // median of 68).  8 took ragged decode from 85.0 to 80.0 us (10 and 12: 81.1, 82.8), the other
 // configurations unchanged.
+#if defined(MX_WG_TIMELINE) && defined(MX_TIMELINE_CHUNK_POSITIONS) && \
+    defined(MX_TIMELINE_UNIT_OVERHEAD)
+// A timeline build may cost the line differently, to compare the workgroup timelines of two
+// line costings from one source.
+constexpr int kChunkPositions = MX_TIMELINE_CHUNK_POSITIONS;
+constexpr int kUnitOverhead = MX_TIMELINE_UNIT_OVERHEAD;
+#else
 constexpr int kChunkPositions = 8;
 constexpr int kUnitOverhead = 8 * kChunkPositions;
+#endif
+static_assert((kChunkPositions & (kChunkPositions - 1)) == 0,
+              "the balanced kernels divide by the chunk weight with a shift");
 // Balanced schedule limits: the largest batch whose seq_lens scan stays within two passes of
 // one workgroup.
-constexpr int64_t kBalancedMaxBatch = 512;
+constexpr int64_t kBalancedMaxBatch = kBalancedBatch;
 constexpr int64_t kBalancedMaxGroups = 4095;  // pieces per unit stay within the 8^4 merge tree
 constexpr int64_t kBalancedMaxUnits = 8192;   // batch * Hkv * row tiles (counter region)
 // The balanced kernels count a batch's chunks (plus per-unit overheads) in 32-bit integers.
@@ -3080,3 +3168,30 @@ const char* mx_last_error(void) { return g_last_error.c_str(); }
 const char* mx_version(void) { return "mxattn 0.1.0 (gfx950 paged GQA decode)"; }
 
 }  // extern "C"
+
+#ifdef MX_WG_TIMELINE
+// Timeline builds only: the per-workgroup stamp table of the current device, kTimelineSlots
+// rows of kTimelineFields unsigned 64-bit values (see WgTimeline).  Synchronous.
+extern "C" int64_t mx_timeline_bytes(void) { return (int64_t)sizeof(g_timeline); }
+
+extern "C" int mx_timeline_clear(void) {
+  void* p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_timeline)) != hipSuccess ||
+      hipMemset(p, 0, sizeof(g_timeline)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+    (void)hipGetLastError();
+    return MX_STATUS_HIP_ERROR;
+  }
+  return MX_STATUS_OK;
+}
+
+extern "C" int mx_timeline_read(void* host, int64_t bytes) {
+  if (host == nullptr || bytes < (int64_t)sizeof(g_timeline)) return MX_STATUS_INVALID_ARGUMENT;
+  void* p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_timeline)) != hipSuccess ||
+      hipMemcpy(host, p, sizeof(g_timeline), hipMemcpyDeviceToHost) != hipSuccess) {
+    (void)hipGetLastError();
+    return MX_STATUS_HIP_ERROR;
+  }
+  return MX_STATUS_OK;
+}
+#endif
