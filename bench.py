@@ -341,6 +341,63 @@ def time_append_attend(spec: W.DecodeSpec, steps: int, warmup: int, seed: int = 
             "note": "value: one launch appends the new token and attends over L keys"}
 
 
+def time_launch_ab(inp: W.DecodeInputs, steps: int, warmup: int) -> dict:
+    """One launch against two for a split-grid workload, same library: phase 0 (the splits
+    merge in-kernel through the arrival-counter tree) and MX_PHASE_MAIN_ONLY then
+    MX_PHASE_COMBINE_ONLY (split kernel, then the combine kernel), interleaved call by call
+    with events around each whole call; medians."""
+    spec = inp.spec
+    stream = torch.cuda.current_stream()
+    nbytes = inp.kv_bytes()
+    copies = (1 if nbytes >= 3 * MALL_BYTES
+              else min(MAX_POOL_COPIES, max(2, math.ceil(3 * MALL_BYTES / max(nbytes, 1)))))
+    pools = [(inp.k_cache, inp.v_cache)] + [(inp.k_cache.clone(), inp.v_cache.clone())
+                                            for _ in range(copies - 1)]
+    plan = pkg.plan(spec.batch, spec.num_heads, spec.num_kv_heads, spec.head_dim,
+                    spec.page_size, spec.max_pages, 0, 0, seqlen_q=spec.seqlen_q)
+    if plan["schedule"] != "split_grid" or plan["splits"] < 2:
+        raise ValueError(f"{spec.name}: the automatic plan is not a split grid with splits")
+    ws = pkg.make_workspace(plan["workspace_bytes"], inp.device)
+    out = torch.empty_like(inp.q)
+    calls = [pkg.BoundDecode(inp.q, k, v, inp.block_table, inp.seq_lens, inp.scale, out=out,
+                             causal=spec.causal, workspace=ws, stream=stream)
+             for k, v in pools]
+    modes = {"one_launch": lambda c: c(_lib.MX_PHASE_ALL),
+             "two_launches": lambda c: (c(_lib.MX_PHASE_MAIN_ONLY),
+                                        c(_lib.MX_PHASE_COMBINE_ONLY))}
+    results = {}
+    for name, fn in modes.items():
+        fn(calls[0])
+        torch.cuda.synchronize()
+        results[name] = out.clone()
+    diff = float((results["one_launch"].float() - results["two_launches"].float()).abs().max())
+    for i in range(warmup):
+        for fn in modes.values():
+            fn(calls[i % len(calls)])
+    ev = {name: [] for name in modes}
+    items = list(modes.items())
+    for i in range(steps):
+        for name, fn in (items if i % 2 == 0 else items[::-1]):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            fn(calls[i % len(calls)])
+            b.record(stream)
+            ev[name].append((a, b))
+    torch.cuda.synchronize()
+    if pkg.read_device_status(ws):
+        raise RuntimeError("device status flags raised during the launch comparison")
+    med = {name: statistics.median(a.elapsed_time(b) * 1e3 for a, b in e)
+           for name, e in ev.items()}
+    return {
+        "metric": "split_grid_one_vs_two_launches_us", "unit": "us", "higher_is_better": False,
+        "n_gpus": 1, "steps": steps, "dtype": "bf16",
+        "config": {"workload": spec.name, "splits": plan["splits"], "pools": copies},
+        "one_launch_us": round(med["one_launch"], 2),
+        "two_launches_us": round(med["two_launches"], 2),
+        "max_abs_diff": diff,
+        "note": "medians of events around whole calls (launches included), interleaved"}
+
+
 def time_shards(inp: W.DecodeInputs, num_shards: int, steps: int, warmup: int) -> dict:
     """The per-GPU pieces of a sharded decode of `inp`, all run on this one GPU: each shard's
     partial decode (shard_pages layout; calls rotate over the shards so no shard is served
@@ -607,6 +664,10 @@ def main(argv=None) -> int:
     ap.add_argument("--shards", type=int, default=0,
                     help="also time the per-GPU pieces of the workload's decode sharded over N "
                          "GPUs' pages (partial decode per shard + merge), on this one GPU")
+    ap.add_argument("--launch-ab", action="store_true",
+                    help="split-grid workloads: time one launch (in-kernel merge tree) against "
+                         "two (split kernel, then combine kernel), interleaved, and print that "
+                         "line only")
     ap.add_argument("--kv-dtype", choices=["bf16", "fp8"], default="bf16",
                     help="fp8: the same workload with K/V rounded to an e4m3fn cache (unit "
                          "scales), decoded by mx_paged_gqa_decode_fp8kv; KV bytes are the fp8 "
@@ -654,6 +715,9 @@ def main(argv=None) -> int:
 
     spec = W.get_spec(args.workload)
     inp = W.make_inputs(spec, seed=args.seed, device="cuda")
+    if args.launch_ab:
+        print(json.dumps(time_launch_ab(inp, args.steps, args.warmup)), flush=True)
+        return 0
     if args.kv_dtype == "fp8":
         inp.k_cache = inp.k_cache.to(torch.float8_e4m3fn)
         inp.v_cache = inp.v_cache.to(torch.float8_e4m3fn)
