@@ -1283,15 +1283,21 @@ __device__ __forceinline__ float load_partial1(const float* p) {
 
 // Arrival of this workgroup at `counter`, which `expected` workgroups reach once each; returns,
 // uniformly over the workgroup, whether it arrived last (and then resets the counter for the
-// next call).  Called by every thread after its partial stores.  The steps:
-//  1. each wave waits until its own stores have completed (s_waitcnt vmcnt(0));
-//  2. the barrier: every wave of the workgroup is past step 1 before thread 0 goes on, so the
-//     stores happen before its increment;
-//  3. thread 0 increments with an agent-scope acq_rel read-modify-write.  Its release half
-//     orders the workgroup's stores before the increment; the acquire half orders the
-//     increments of the earlier arrivals (and so their stores) before what follows;
-//  4. the barrier hands thread 0's result, and the acquire, to every thread before any loads
-//     the last arrival makes of the others' partials.
+// next call).  Called by every thread after its partial stores (store_partial4/1).  The steps:
+//  1. each wave waits until its own stores have completed (s_waitcnt vmcnt(0)): with sc1 they
+//     are then written through to the device-coherent level, past the XCD's own L2;
+//  2. the barrier: every wave of the workgroup is past step 1 before thread 0 goes on, so all
+//     of the workgroup's stores are complete before its increment is issued;
+//  3. thread 0 increments with a relaxed agent-scope read-modify-write, performed at the
+//     device-coherent level: the value returned counts the increments before it, each issued
+//     after its workgroup's stores were complete;
+//  4. the barrier hands thread 0's result to every thread, so the last arrival issues its
+//     loads of the others' partials (load_partial4/1, sc1: served from the device-coherent
+//     level) only after the read-modify-write has returned.
+// The partials never sit in a non-coherent cache line (stores write through, loads do not hit
+// stale lines), which is why no release or acquire fence is needed; an acq_rel increment adds
+// an L2 write-back and invalidate per arrival and measured 98.6 against 86.2 us on ragged
+// decode.
 __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected, int* s_flag) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);
