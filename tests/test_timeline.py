@@ -1,0 +1,62 @@
+"""The per-workgroup timeline tool's host side: the summary of one launch's stamp table, and the
+timeline build's line costings (no GPU, no compilation)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from mx_flash_attn_kernel_opt__amd import timeline as T
+
+
+def _table(rows):
+    """A stamp table (kTimelineSlots rows of FIELDS) with `rows` in its first slots."""
+    t = np.zeros((16384, len(T.FIELDS)), dtype=np.uint64)
+    for i, r in enumerate(rows):
+        t[i] = r
+    return t
+
+
+def test_summary_times_are_microseconds_after_the_first_entry():
+    # 100 ticks = 1 us; workgroup 1 enters last, workgroup 2 streams nothing.
+    rows = [(1000, 1200, 6000, 6100, 0, 2),
+            (1100, 1400, 9000, 9500, 1, 1),
+            (1050, 0, 0, 1300, 2, 0)]
+    s = T.summarize(_table(rows))
+    assert s["workgroups"] == 3 and s["streaming_workgroups"] == 2
+    assert s["entry_pct_0_10_50_90_100"][0] == 0.0
+    assert s["entry_pct_0_10_50_90_100"][4] == 1.0            # (1100 - 1000) / 100
+    assert s["exit_pct"][4] == 85.0                             # (9500 - 1000) / 100
+    assert s["exit_pct"][0] == 3.0                              # the empty workgroup
+    # streaming percentiles ignore workgroups that streamed nothing
+    assert s["stream_begin_pct"][0] == 2.0 and s["stream_begin_pct"][4] == 4.0
+    assert s["stream_end_pct"][4] == 80.0
+    assert s["tail_us"] == pytest.approx(85.0 - 51.0)           # max exit - median exit
+    assert s["latest"][0] == {"wg": 1, "xcd": 1, "pieces": 1, "stream_begin": 4.0,
+                              "stream_end": 80.0, "exit": 85.0}
+    assert s["per_xcd"]["1"] == {"workgroups": 1, "entry_median": 1.0, "exit_median": 85.0,
+                                 "exit_max": 85.0}
+
+
+def test_summary_keeps_workgroup_ids_of_sparse_tables():
+    t = np.zeros((16384, len(T.FIELDS)), dtype=np.uint64)
+    t[7] = (500, 600, 700, 800, 3, 1)
+    t[4000] = (400, 500, 2400, 2500, 6, 4)
+    s = T.summarize(t)
+    assert [x["wg"] for x in s["latest"]] == [4000, 7]
+    assert s["pieces_pct"] == [1, 2, 4]
+
+
+def test_empty_table_is_an_error():
+    with pytest.raises(ValueError):
+        T.summarize(np.zeros((16384, len(T.FIELDS)), dtype=np.uint64))
+
+
+def test_line_costings_are_powers_of_two_per_chunk():
+    # The balanced kernels divide by the positions per chunk with a shift (static_assert in
+    # csrc/paged_decode.hip), so every timeline build's costing must keep it a power of two.
+    for tag, (per_chunk, per_unit) in T.LINE_COSTS.items():
+        assert per_chunk & (per_chunk - 1) == 0, tag
+        assert per_unit >= 0
+        assert T.lib_path(tag).endswith(f"libmxattn_timeline_{tag}.so")
+    assert T.LINE_COSTS["line8"] == (8, 64)    # the shipped costing
