@@ -76,6 +76,9 @@ extern "C" {
  * verify_real.py:12-14 / bench_all.py:98-100 as argtypes [c_void_p]*6 + [c_int64]*9.
  *   - scale is derived as 1/sqrt(headdim) (submission_clean.cu:451);
  *   - block_table row width = num_blocks / batch_size (submission_clean.cu:449, task.md:61);
+ *   - the K/V pools hold num_blocks pages (task.md:57-58): page ids outside [0, num_blocks)
+ *     are flagged (MX_DEVICE_BAD_PAGE_ID) and read as page 0, where the reference reads
+ *     outside the pool;
  *   - seqlen_k is the capacity used for split planning (task.md:7, 131);
  *   - launches on the legacy default stream, no synchronisation (task.md:67);
  *   - uses a library-owned, grow-only workspace per device (submission_clean.cu:478-491);

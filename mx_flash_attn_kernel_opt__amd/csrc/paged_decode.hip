@@ -3000,11 +3000,12 @@ void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_pa
     st = fail(MX_STATUS_INVALID_SHAPE, "run_kernel: headdim must be >= 1");
   } else {
     const float scale = 1.0f / sqrtf((float)headdim);
-    // The legacy ABI carries no pool size (num_blocks is the table row width times batch),
-    // so only negative page ids are flagged.
+    // num_blocks is both the pool size (k_cache_paged holds num_blocks pages, task.md:57-58)
+    // and the table's size (num_blocks / batch_size entries per row, task.md:61): page ids
+    // outside [0, num_blocks) are flagged and read as page 0.
     st = mx_paged_gqa_decode(q, k_cache_paged, v_cache_paged, output, cache_seqlens,
                              block_table, batch_size, seqlen_q, num_heads, num_heads_k, headdim,
-                             page_block_size, 0, num_blocks / batch_size, seqlen_k,
+                             page_block_size, num_blocks, num_blocks / batch_size, seqlen_k,
                              (int32_t)causal, scale, 0, nullptr, 0, 0, nullptr);
   }
   if (st != MX_STATUS_OK) fprintf(stderr, "run_kernel: %s\n", g_last_error.c_str());

@@ -391,6 +391,30 @@ def test_bad_page_id_is_flagged_not_read(ns):
     _check(inp, out, batches=[0], label="unaffected sequence")
 
 
+def test_run_kernel_bounds_page_ids_by_num_blocks():
+    """run_kernel takes num_blocks as the pool size (task.md:57-58): an id in a valid slot at or
+    past num_blocks is flagged and read as page 0.  The tensors hold 16 pages, more than the
+    10 run_kernel is told of, so the id stays inside the allocation either way."""
+    spec = W.custom_spec("rk_badpage", [40, 70], 32, 8, 128, 16, max_pages=5, pool_pages=16)
+    inp = W.make_inputs(spec, seed=15, device=DEV)
+    bt = inp.block_table.clone()
+    num_blocks = 2 * 5
+    bt[0] = torch.arange(0, 5, dtype=torch.int32, device=DEV)
+    bt[1] = torch.arange(5, 10, dtype=torch.int32, device=DEV)
+    bt[1, 2] = num_blocks + 2              # a valid slot (70 tokens use 5 pages)
+    out = torch.zeros_like(inp.q)
+    read_device_status()                   # clear what earlier calls left in the library's word
+    run_kernel(inp.q, inp.k_cache, inp.v_cache, out, inp.seq_lens, bt,
+               2, 80, 1, 32, 8, 128, 16, num_blocks, 0)
+    torch.cuda.synchronize()
+    assert read_device_status() & 1        # MX_DEVICE_BAD_PAGE_ID
+    as_read = bt.clone()
+    as_read[1, 2] = 0
+    ref = paged_decode_reference(inp.q.cpu(), inp.k_cache.cpu(), inp.v_cache.cpu(),
+                                 as_read.cpu(), inp.seq_lens.cpu(), inp.scale)
+    assert_close_to_oracle(out, ref, "run_kernel out-of-pool id read as page 0")
+
+
 @pytest.mark.parametrize("ns", [0, 1])
 def test_sequence_longer_than_planned_capacity_is_flagged(ns):
     spec = W.custom_spec("toolong", [100, 500], 32, 8, 128, 16, max_pages=32)
