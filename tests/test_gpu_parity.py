@@ -313,6 +313,25 @@ def test_balanced_repeated_calls_are_identical():
     assert read_device_status(ws) == 0
 
 
+@pytest.mark.parametrize("name,ns", [("ragged", 0), ("long_b1_32k", 0), ("long_b4_32k", 0)])
+def test_merge_trees_are_placement_independent(name, ns):
+    """The first workgroup of a launch lands on whichever XCD the hardware queue's rotation
+    reached, so a kernel run before a call moves every workgroup to another XCD.  Calls after
+    kernels of 23 different grid sizes give bitwise-identical outputs: the cross-XCD handoff
+    of the merge trees (balanced cut units, split-grid splits) does not depend on where the
+    pieces ran."""
+    inp = W.make_inputs(name, seed=21, device=DEV)
+    ws = torch.zeros(1 << 24, dtype=torch.uint8, device=DEV)
+    junk = torch.empty(1 << 22, device=DEV)
+    first = _decode(inp, num_splits=ns, workspace=ws).clone()
+    for k in range(1, 24):
+        junk[: k * 4099].fill_(float(k))    # a kernel of a varying grid before the call
+        out = _decode(inp, num_splits=ns, workspace=ws)
+        assert torch.equal(out, first), f"{name}: output changed after a {k}-step shift"
+    _check(inp, first, _sample(inp.spec.batch, 32), label=f"{name} placement")
+    assert read_device_status(ws) == 0
+
+
 def test_balanced_deep_merge_tree():
     """One unit cut into ~4000 pieces: a four-level fan-in-8 merge."""
     spec = W.custom_spec("deep", [70000], 8, 1, 64, 16)
