@@ -355,7 +355,7 @@ def time_launch_ab(inp: W.DecodeInputs, steps: int, warmup: int) -> dict:
                                             for _ in range(copies - 1)]
     plan = pkg.plan(spec.batch, spec.num_heads, spec.num_kv_heads, spec.head_dim,
                     spec.page_size, spec.max_pages, 0, 0, seqlen_q=spec.seqlen_q)
-    if plan["schedule"] != "split_grid" or plan["splits"] < 2:
+    if plan["schedule"] == "balanced" or plan["splits"] < 2:
         raise ValueError(f"{spec.name}: the automatic plan is not a split grid with splits")
     ws = pkg.make_workspace(plan["workspace_bytes"], inp.device)
     out = torch.empty_like(inp.q)

@@ -63,6 +63,10 @@ extern "C" {
 #define MX_SCHEDULE_BALANCED 1     /* one launch of a fixed number of workgroups that divide the
                                       batch's K/V chunks evenly from seq_lens on the device and
                                       merge split sequences themselves                            */
+#define MX_SCHEDULE_SPLIT_GRID_PAIRED 2 /* the split grid over pairs of adjacent KV heads, two
+                                      waves of each workgroup per head (automatic splits of
+                                      >= 1024 tokens, head_dim 128, bf16 cache, no fused
+                                      append, 2 * seqlen_q * group <= 16)                         */
 
 /* Phase flags for mx_paged_gqa_decode (0 = run everything). */
 #define MX_PHASE_MAIN_ONLY 1        /* split grid: run only the split-KV kernel, partials stay in

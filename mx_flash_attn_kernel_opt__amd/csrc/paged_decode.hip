@@ -849,6 +849,31 @@ __device__ __forceinline__ void publish_wave_state(char* lds, const SoftmaxState
   __syncthreads();
 }
 
+// merged_head for a workgroup whose waves stream two stored KV heads (mx_paged_decode_splitkv
+// with kPairW): row hh of the kernel head, whose rows of each query token are the stored first
+// head's `g` rows then the second's, merges the states of the two waves that streamed its own
+// head (waves 0-1 the first, 2-3 the second).
+template <int D>
+__device__ __forceinline__ f32x4 merged_head_pair(const char* lds, int hh, int d, float& lse,
+                                                  const MainShape& sh) {
+  using L = GroupLds<D, 4, 1>;
+  const float* sm = L::m(const_cast<char*>(lds));
+  const float* sl = L::l(const_cast<char*>(lds));
+  const int w0 = hh - row_token(hh, sh) * sh.group >= sh.group / 2 ? 2 : 0;
+  const int s0 = w0 * L::kRows + hh;
+  const int s1 = s0 + L::kRows;
+  const float mx = fmaxf(sm[s0], sm[s1]);
+  const float a0 = __builtin_amdgcn_exp2f(sm[s0] - mx);
+  const float a1 = __builtin_amdgcn_exp2f(sm[s1] - mx);
+  const float lsum = a0 * sl[s0] + a1 * sl[s1];
+  const float* so = L::o(const_cast<char*>(lds));
+  const f32x4 acc = a0 * *reinterpret_cast<const f32x4*>(so + s0 * L::kRow + d) +
+                    a1 * *reinterpret_cast<const f32x4*>(so + s1 * L::kRow + d);
+  const bool seen = lsum > 0.f;
+  lse = seen ? mx + log2f(lsum) : -INFINITY;
+  return acc * (seen ? 1.0f / lsum : 0.f);
+}
+
 // Merged (normalised) dims d..d+3 of row slot hh (< 16*KT) and its log2-sum-exp; a row that
 // saw no key (l == 0: causal rows before their first key) is zeros with log2-sum-exp -inf.
 template <int D, int NW, int KT>
@@ -1318,34 +1343,41 @@ __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected
 // slots gslot + t * stride, merged as
 //   O = sum_t 2^(lse_t - M) O_t / sum_t 2^(lse_t - M),  lse = M + log2 sum_t 2^(lse_t - M),
 // M = max_t lse_t (optimized_c500_flash_attn.cu:666-728, log2 domain).  A row no item saw a key
-// for (every lse -inf: causal rows before their first key) stays zeros with lse -inf.  Each
-// thread issues the loads of all items for its dims at once (unconditional: slots past the
-// group re-read its first item and are masked by their lse), so a step is one memory round
-// trip.  The merged rows go to the output (`final`) or to the group's first slot (lse to s_lse,
-// which the caller stores after a barrier).
-template <int D, int NW, int W, class Tree>
-__device__ __forceinline__ void merge_group(const Tree& tree, int gslot, int stride, int gsize,
-                                            int nrows, bool final, float* s_lse) {
-  // An opaque copy of the thread index: keeps the per-thread addressing of this step from being
-  // hoisted out of the callers' loops, where it would stay live across the chunk streaming.
-  int tid = threadIdx.x;
-  asm volatile("" : "+v"(tid));
-  for (int e = tid; e < nrows * (D / 4); e += 64 * NW) {
-    const int hh = e / (D / 4);
-    const int d = 4 * (e - hh * (D / 4));
-    float ls[W];
-    f32x4 vs[W];
+// for (every lse -inf: causal rows before their first key) stays zeros with lse -inf.  The
+// merged rows go to the output (`final`) or to the group's first slot (lse to s_lse, which the
+// caller stores after a barrier).
+//
+// merge_elems handles E four-dim elements e0, e0 + 64*NW, ... (< total) of the group's rows: it
+// issues the loads of all items for all of them at once (unconditional: slots past the group
+// re-read its first item and are masked by their lse, elements past the rows re-read e0's), so
+// the step is one memory round trip.
+template <int D, int NW, int W, int E, class Tree>
+__device__ __forceinline__ void merge_elems(const Tree& tree, int e0, int total, int gslot,
+                                            int stride, int gsize, bool final, float* s_lse) {
+  float ls[E][W];
+  f32x4 vs[E][W];
+  int hh[E], d[E];
+#pragma unroll
+  for (int q = 0; q < E; ++q) {
+    const int e = e0 + q * 64 * NW;
+    const int ee = e < total ? e : e0;
+    hh[q] = ee / (D / 4);
+    d[q] = 4 * (ee - hh[q] * (D / 4));
 #pragma unroll
     for (int t = 0; t < W; ++t) {
       const int sl = gslot + (t < gsize ? t : 0) * stride;
-      ls[t] = load_partial1(tree.lse(hh, sl));
-      vs[t] = load_partial4(tree.o(hh, sl) + d);
+      ls[q][t] = load_partial1(tree.lse(hh[q], sl));
+      vs[q][t] = load_partial4(tree.o(hh[q], sl) + d[q]);
     }
+  }
+#pragma unroll
+  for (int q = 0; q < E; ++q) {
+    if (e0 + q * 64 * NW >= total) break;
     float mx = -INFINITY;
 #pragma unroll
     for (int t = 0; t < W; ++t) {
-      if (t >= gsize) ls[t] = -INFINITY;
-      mx = fmaxf(mx, ls[t]);
+      if (t >= gsize) ls[q][t] = -INFINITY;
+      mx = fmaxf(mx, ls[q][t]);
     }
     const bool seen = mx > -INFINITY;
     const float mref = seen ? mx : 0.f;
@@ -1353,18 +1385,37 @@ __device__ __forceinline__ void merge_group(const Tree& tree, int gslot, int str
     float wsum = 0.f;
 #pragma unroll
     for (int t = 0; t < W; ++t) {
-      const float w = __builtin_amdgcn_exp2f(ls[t] - mref);  // 0 for t >= gsize
+      const float w = __builtin_amdgcn_exp2f(ls[q][t] - mref);  // 0 for t >= gsize
       wsum += w;
-      acc += w * vs[t];
+      acc += w * vs[q][t];
     }
     acc *= seen ? 1.0f / wsum : 0.f;
     const float lse = seen ? mx + log2f(wsum) : -INFINITY;
     if (final) {
-      tree.store(hh, d, acc, lse);
+      tree.store(hh[q], d[q], acc, lse);
     } else {
-      store_partial4(tree.o(hh, gslot) + d, acc);
-      if (d == 0) s_lse[hh] = lse;
+      store_partial4(tree.o(hh[q], gslot) + d[q], acc);
+      if (d[q] == 0) s_lse[hh[q]] = lse;
     }
+  }
+}
+
+// The whole step: nrows * D/4 elements over the workgroup's 64*NW threads, two per thread and
+// round when there are more elements than threads (16 rows at D=128 take one round instead of
+// two: two round trips per level lengthened the tail of paired-head split grids by ~2 us).
+template <int D, int NW, int W, class Tree>
+__device__ __forceinline__ void merge_group(const Tree& tree, int gslot, int stride, int gsize,
+                                            int nrows, bool final, float* s_lse) {
+  // An opaque copy of the thread index: keeps the per-thread addressing of this step from being
+  // hoisted out of the callers' loops, where it would stay live across the chunk streaming.
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int total = nrows * (D / 4);
+  if (total > 64 * NW) {
+    for (int e0 = tid; e0 < total; e0 += 2 * 64 * NW)
+      merge_elems<D, NW, W, 2>(tree, e0, total, gslot, stride, gsize, final, s_lse);
+  } else if (tid < total) {
+    merge_elems<D, NW, W, 1>(tree, tid, total, gslot, stride, gsize, final, s_lse);
   }
 }
 
@@ -1463,7 +1514,17 @@ struct SplitTree {
 // split and row.  With fused_combine the splits of each unit merge them through an in-kernel
 // tree (merge_tree: groups of kMergeFanIn splits, the last arrival of a group merges it), so the
 // whole call is one launch; otherwise mx_paged_decode_combine merges them in a second launch.
-template <int D, int NBUF, int NW, bool kCausal, int KT, bool kAppend, bool kFp8>
+//
+// kPairW (MX_SCHEDULE_SPLIT_GRID_PAIRED): kernel head p is the stored KV heads 2p and 2p+1, whose
+// rows of one token are adjacent.  Waves 0-1 stream head 2p and waves 2-3 head 2p+1 over the same
+// chunks of the split (wave wv takes chunks c0 + (wv & 1), c0 + (wv & 1) + 2, ...), each wave with
+// the query rows of both heads, of which only its own head's rows are merged (merged_head_pair).
+// The unit's rows are the two heads' rows; the strides in MainShape are the stored heads'.  A
+// workgroup streaming one head's 256-byte rows reads more slowly the rows at some offsets in
+// the 2 KB token row than at others when every head is streamed at once; two adjacent heads
+// per workgroup even that out (the measurements are beside make_plan).
+template <int D, int NBUF, int NW, bool kCausal, int KT, bool kAppend, bool kFp8,
+          bool kPairW = false>
 __global__ __launch_bounds__(64 * NW)
 __attribute__((amdgpu_waves_per_eu(min_waves_per_simd<D, KT>())))
 void mx_paged_decode_splitkv(
@@ -1538,6 +1599,11 @@ void mx_paged_decode_splitkv(
     stream_chunks<D, NBUF, NW, kCausal, KT, NewTokens<kFp8>, kFp8>(st, qop, kc, vc, bt_row, kv, c_lo, c_end, ext.cache,
                                             c_mask, row_lim, wv, L::ktile(lds, wv), sh, bad_page,
                                             nt);
+  } else if constexpr (kPairW) {
+    static_assert(NW == 4 && KT == 1 && !kAppend, "paired waves: four waves, one row tile");
+    stream_chunks<D, NBUF, 2, kCausal, KT, NoExtraChunk, kFp8>(
+        st, qop, kc, vc, bt_row, 2 * kv + (wv >> 1), c_lo, c_end, ext.cache, c_mask, row_lim,
+        wv & 1, L::ktile(lds, wv), sh, bad_page);
   } else {
     stream_chunks<D, NBUF, NW, kCausal, KT, NoExtraChunk, kFp8>(
         st, qop, kc, vc, bt_row, kv, c_lo, c_end, ext.cache, c_mask, row_lim, wv,
@@ -1551,7 +1617,11 @@ void mx_paged_decode_splitkv(
     const int hh = e / (D / 4);
     const int d = 4 * (e - hh * (D / 4));
     float lse;
-    const f32x4 o = merged_head<D, NW, KT>(lds, hh, d, lse);
+    f32x4 o;
+    if constexpr (kPairW)
+      o = merged_head_pair<D>(lds, hh, d, lse, sh);
+    else
+      o = merged_head<D, NW, KT>(lds, hh, d, lse);
     const int64_t row = row_base(b, kv, sh) + row_offset(r0 + hh, sh);
     if (single) {
       store_row4<D>(out, sh, row, d, o, lse);
@@ -2132,6 +2202,7 @@ int64_t align_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 //    kMinTokensPerSplit long and at most kMaxTokensPerSplit.
 constexpr int64_t kMinTokensPerSplit = 128;   // amortises Q load, pipeline fill and partials
 constexpr int64_t kMaxTokensPerSplit = 16384;  // bounds one workgroup's share of a sequence
+constexpr int64_t kPairMinTokensPerSplit = 1024;  // paired split grid: shortest paired split
 constexpr int64_t kMaxGridDim = 65535;
 // Query heads per KV head (MQA included).  Rows of one KV head are processed in 16- or 32-row
 // groups whatever the group size, so the limit only bounds how often K/V is re-streamed.
@@ -2192,6 +2263,11 @@ struct Plan {
   int chunk_shift = 0;
 };
 
+// KV heads of the kernels' units: pairs of the (kernel) heads on the paired split grid.
+int64_t plan_kv_heads(const Plan& plan, int64_t kv_heads) {
+  return plan.schedule == MX_SCHEDULE_SPLIT_GRID_PAIRED ? kv_heads / 2 : kv_heads;
+}
+
 int query_num_cus(int64_t* num_cus) {
   static std::mutex mu;
   static std::vector<int> cache;
@@ -2216,9 +2292,25 @@ int query_num_cus(int64_t* num_cus) {
 }
 
 // Validates the shape and computes the split plan.  Performs no HIP call when num_cus > 0.
+// Automatic split count of the split grid: enough splits for `slots` resident workgroups over
+// `units` units, each split holding at least kMinTokensPerSplit tokens at capacity `cap` (and
+// splitting starts at four splits: the partial round trip and merge, ~3.5 us, are only repaid
+// by cutting a unit's streaming time at least four ways; capacity 256: 1 split 7.8-8.1 us, 2
+// splits 8.7-8.9 us; capacity 512 with 64 units: 4 splits 9.2 us, 1 split 10.2 us), and at most
+// kMaxTokensPerSplit.
+int64_t auto_splits(int64_t units, int64_t slots, int64_t cap) {
+  int64_t ns = ceil_div(slots, units);
+  int64_t max_by_len = cap / kMinTokensPerSplit;
+  if (max_by_len < 4) max_by_len = 1;
+  if (ns > max_by_len) ns = max_by_len;
+  const int64_t min_by_len = ceil_div(cap, kMaxTokensPerSplit);
+  if (ns < min_by_len) ns = min_by_len;
+  return ns;
+}
+
 int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads,
               int64_t head_dim, int64_t page_size, int64_t max_pages, int64_t max_seq_len,
-              int64_t num_splits, int64_t num_cus, Plan* plan) {
+              int64_t num_splits, int64_t num_cus, bool pair_ok, Plan* plan) {
   if (batch < 1 || seqlen_q < 1 || num_heads < 1 || num_kv_heads < 1 || head_dim < 1 ||
       page_size < 1 || max_pages < 1)
     return fail(MX_STATUS_INVALID_SHAPE,
@@ -2269,21 +2361,11 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
       const int st = query_num_cus(&num_cus);
       if (st != MX_STATUS_OK) return st;
     }
-    const int64_t units = batch * num_kv_heads * row_tiles;
-    ns = ceil_div(num_cus * groups_per_cu(head_dim), units);
-    // Every split holds at least kMinTokensPerSplit tokens at capacity, and splitting starts
-    // at four splits: the partial round trip and merge (~3.5 us) are only repaid by cutting a
-    // unit's streaming time at least four ways (capacity 256: 1 split 7.8-8.1 us, 2 splits
-    // 8.7-8.9 us; capacity 512 with 64 units: 4 splits 9.2 us, 1 split 10.2 us).
-    int64_t max_by_len = cap / kMinTokensPerSplit;
-    if (max_by_len < 4) max_by_len = 1;
-    if (ns > max_by_len) ns = max_by_len;
-    const int64_t min_by_len = ceil_div(cap, kMaxTokensPerSplit);
-    if (ns < min_by_len) ns = min_by_len;
+    ns = auto_splits(batch * num_kv_heads * row_tiles, num_cus * groups_per_cu(head_dim), cap);
   }
   if (ns > cap_pages) ns = cap_pages;
   if (ns < 1) ns = 1;
-  const int64_t pages_per_split = ceil_div(cap_pages, ns);
+  int64_t pages_per_split = ceil_div(cap_pages, ns);
   ns = ceil_div(cap_pages, pages_per_split);  // page-aligned splits, none empty at capacity
   if (ns > kMaxGridDim) return fail(MX_STATUS_UNSUPPORTED, "split count exceeds 65535");
 
@@ -2331,6 +2413,33 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
     return fail(MX_STATUS_UNSUPPORTED,
                 "the balanced schedule supports batch <= 512, batch * num_kv_heads * row "
                 "groups <= 8192 and fewer than 2^30 chunks of capacity over all units");
+  // Paired heads (MX_SCHEDULE_SPLIT_GRID_PAIRED, mx_paged_decode_splitkv with kPairW): units of
+  // two adjacent KV heads, streamed two waves per head, when the split grid runs automatically
+  // and each workgroup still streams >= kPairMinTokensPerSplit tokens.  A workgroup streaming one
+  // 256-byte head row per token reads rows at some offsets of the 2 KB token row more slowly
+  // than others while every head streams: on long B=4 at 128K the heads' workgroups ended
+  // 267-332 us apart, paired 290-303 us.  Interleaved A/B against one head per workgroup: long
+  // B=4 128K 329.7 against 349.1 us, B=1 128K 91.5 against 94.5, B=4 32K 90.5 against 92.5.
+  // Shorter splits lose: B=1 at 32K (512 tokens per paired split) 31.1 against 30.0 us, where
+  // the tree's partials of 16 rows lengthen the merge tail.
+  if (pair_ok && num_splits == 0 && head_dim == 128 && num_kv_heads % 2 == 0 &&
+      2 * rows <= 16) {
+    int64_t ns2 = auto_splits(batch * (num_kv_heads / 2), num_cus * groups_per_cu(head_dim), cap);
+    if (ns2 > cap_pages) ns2 = cap_pages;
+    if (ns2 < 1) ns2 = 1;
+    const int64_t pages2 = ceil_div(cap_pages, ns2);
+    ns2 = ceil_div(cap_pages, pages2);
+    if (ns2 > 1 && pages2 * page_size >= kPairMinTokensPerSplit) {
+      plan->schedule = MX_SCHEDULE_SPLIT_GRID_PAIRED;
+      ns = ns2;
+      pages_per_split = pages2;
+      plan->splits = ns;
+      plan->tokens_per_split = pages_per_split * page_size;
+      plan->cap_tokens = std::min<int64_t>(table_tokens, ns * plan->tokens_per_split);
+      plan->rows = 2 * rows;
+    }
+  }
+  if (ns > kMaxGridDim) return fail(MX_STATUS_UNSUPPORTED, "split count exceeds 65535");
   if (ns > 1) {
     const int64_t prow = batch * seqlen_q * num_heads * ns;
     plan->lse_offset = kPartialBase;
@@ -2454,11 +2563,14 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   constexpr int kNBUF = ring_depth<D>();
   constexpr int kNBUF8 = ring_depth_fp8<D>();
   MainShape sh;
+  // Strides are the stored heads'; the paired split grid's kernel heads are pairs of them.
+  const bool paired = plan.schedule == MX_SCHEDULE_SPLIT_GRID_PAIRED;
+  const int64_t kernel_kv = plan_kv_heads(plan, num_kv_heads);
   sh.page_stride = page_size * num_kv_heads * D;
   sh.token_stride = (int)(num_kv_heads * D);
   sh.num_heads = (int)num_heads;
-  sh.num_kv_heads = (int)num_kv_heads;
-  sh.group = (int)(num_heads / num_kv_heads);
+  sh.num_kv_heads = (int)kernel_kv;
+  sh.group = (int)(num_heads / kernel_kv);
   sh.group_magic = sh.group == 1 ? 0u : (uint32_t)((1ull << 32) / (uint64_t)sh.group + 1);
   if (pair_group > 0 && D != 128) return hipErrorInvalidValue;
   sh.pair_group = pair_group;
@@ -2526,18 +2638,26 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   // One launch (the splits of each unit merge through an in-kernel tree) when the units' arrival
   // counters fit the counter region and the caller did not ask for the two phases separately.
   const bool fused = phase == 0 && plan.splits > 1 &&
-                     split_tree_fits(batch * num_kv_heads * plan.row_tiles, plan.splits);
+                     split_tree_fits(batch * kernel_kv * plan.row_tiles, plan.splits);
   sh.split_groups = (int)ceil_div(plan.splits, kMergeFanIn);
   sh.fused_combine = fused ? 1 : 0;
   if (phase != MX_PHASE_COMBINE_ONLY) {
-    const dim3 grid((unsigned)(num_kv_heads * plan.row_tiles), (unsigned)batch,
+    const dim3 grid((unsigned)(kernel_kv * plan.row_tiles), (unsigned)batch,
                     (unsigned)plan.splits);
     auto go = [&](auto kernel, auto kc, auto vc) {
       hipLaunchKernelGGL(kernel, grid, dim3(64 * kNW), 0, stream, q16, kc, vc,
                          static_cast<uint16_t*>(out), seq_lens, block_table, part_o, part_lse,
                          reinterpret_cast<uint32_t*>(ws + kStatusBytes), status, sh);
     };
-    if (kv.fp8 && append)
+    if (paired) {
+      // make_plan pairs only bf16 decodes without a fused append, at head_dim 128, one tile.
+      if constexpr (D == 128 && KT == 1) {
+        if (kv.fp8 || append) return hipErrorInvalidValue;
+        go(mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT, false, false, true>, k16, v16);
+      } else {
+        return hipErrorInvalidValue;
+      }
+    } else if (kv.fp8 && append)
       go(mx_paged_decode_splitkv<D, kNBUF8, kNW, kCausal, KT, true, true>, k8, v8);
     else if (kv.fp8)
       go(mx_paged_decode_splitkv<D, kNBUF8, kNW, kCausal, KT, false, true>, k8, v8);
@@ -2578,7 +2698,7 @@ static int report_plan(bool fp8, int64_t batch, int64_t seqlen_q, int64_t num_he
   Plan plan;
   const KernelHeads kh = kernel_heads(seqlen_q, num_heads, num_kv_heads, head_dim, fp8);
   const int st = make_plan(batch, seqlen_q, num_heads, kh.kv_heads, kh.head_dim, page_size,
-                           max_pages_per_seq, max_seq_len, num_splits, num_cus, &plan);
+                           max_pages_per_seq, max_seq_len, num_splits, num_cus, !fp8, &plan);
   if (st != MX_STATUS_OK) return st;
   if (schedule_out) *schedule_out = plan.schedule;
   if (splits_out) *splits_out = plan.splits;
@@ -2586,7 +2706,7 @@ static int report_plan(bool fp8, int64_t batch, int64_t seqlen_q, int64_t num_he
   if (workgroups_out)
     *workgroups_out = plan.schedule == MX_SCHEDULE_BALANCED
                           ? plan.groups
-                          : batch * kh.kv_heads * plan.row_tiles * plan.splits;
+                          : batch * plan_kv_heads(plan, kh.kv_heads) * plan.row_tiles * plan.splits;
   if (workspace_bytes_out) *workspace_bytes_out = plan.workspace_bytes;
   return ok();
 }
@@ -2623,7 +2743,7 @@ int64_t mx_paged_gqa_decode_workspace_size(int64_t batch, int64_t seqlen_q, int6
     Plan plan;
     const KernelHeads kh = kernel_heads(seqlen_q, num_heads, num_kv_heads, head_dim, fp8);
     const int st = make_plan(batch, seqlen_q, num_heads, kh.kv_heads, kh.head_dim, page_size,
-                             max_pages_per_seq, max_seq_len, num_splits, 0, &plan);
+                             max_pages_per_seq, max_seq_len, num_splits, 0, !fp8, &plan);
     if (st != MX_STATUS_OK) return st;
     bytes = std::max(bytes, plan.workspace_bytes);
   }
@@ -2641,7 +2761,7 @@ int prepare_decode(const void* q, const void* k_cache, const void* v_cache, cons
                    int64_t head_dim, int64_t page_size, int64_t num_pages,
                    int64_t max_pages_per_seq, int64_t max_seq_len, int32_t causal, float scale,
                    int64_t num_splits, void** workspace, int64_t workspace_bytes,
-                   int32_t phase, void* stream, Plan* plan) {
+                   int32_t phase, void* stream, bool pair_ok, Plan* plan) {
   if (phase != 0 && phase != MX_PHASE_MAIN_ONLY && phase != MX_PHASE_COMBINE_ONLY)
     return fail(MX_STATUS_INVALID_ARGUMENT, "phase must be 0, 1 or 2");
   // The kernels read q, K and V rows as 16-byte vectors and write out in 8-byte pieces.
@@ -2654,7 +2774,7 @@ int prepare_decode(const void* q, const void* k_cache, const void* v_cache, cons
   if (!std::isfinite(scale)) return fail(MX_STATUS_INVALID_ARGUMENT, "scale must be finite");
   if (num_pages < 0) return fail(MX_STATUS_INVALID_SHAPE, "num_pages must be >= 0");
   int st = make_plan(batch, seqlen_q, num_heads, num_kv_heads, head_dim, page_size,
-                     max_pages_per_seq, max_seq_len, num_splits, 0, plan);
+                     max_pages_per_seq, max_seq_len, num_splits, 0, pair_ok, plan);
   if (st != MX_STATUS_OK) return st;
   if (*workspace != nullptr) {
     if (workspace_bytes < plan->workspace_bytes)
@@ -2718,7 +2838,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* o
   const int st = prepare_decode(q, k_cache, v_cache, out, batch, seqlen_q, num_heads,
                                 kh.kv_heads, kh.head_dim, page_size, num_pages, max_pages_per_seq,
                                 max_seq_len, causal, scale, num_splits, &workspace,
-                                workspace_bytes, phase, stream, &plan);
+                                workspace_bytes, phase, stream, !kv.fp8, &plan);
   if (st != MX_STATUS_OK) return st;
   return run_decode(plan, q, k_cache, v_cache, out, o_out, lse_out, seq_lens, block_table, batch,
                     seqlen_q, num_heads, kh.kv_heads, kh.head_dim, page_size, num_pages,
@@ -3074,7 +3194,7 @@ static int decode_append_impl(const void* q, const void* k_new, const void* v_ne
   const KernelHeads kh = kernel_heads(seqlen_q, num_heads, num_kv_heads, head_dim, kv.fp8);
   st = prepare_decode(q, k_cache, v_cache, out, batch, seqlen_q, num_heads, kh.kv_heads,
                       kh.head_dim, page_size, num_pages, max_pages_per_seq, max_seq_len, causal,
-                      scale, num_splits, &workspace, workspace_bytes, 0, stream, &plan);
+                      scale, num_splits, &workspace, workspace_bytes, 0, stream, false, &plan);
   if (st != MX_STATUS_OK) return st;
   AppendArgs app;
   if (seqlen_new >= 1 && seqlen_new <= kChunk) {

@@ -38,12 +38,16 @@ def _workspace(inp, num_splits):
 MANY_UNITS = [40 + (b % 7) for b in range(1600)]   # 12 800 units: more than the counters
 
 
+PAIRED = [0, 1, 17, 1025, 9000, 16384]            # few long units: the paired split grid
+
+
 @pytest.mark.parametrize("num_splits,schedule,launches", [
     (0, "balanced", 1),      # merge tree with arrival counters reset in-kernel
     (4, "split_grid", 1),    # one-level split tree (arrival counters reset by it)
     (32, "split_grid", 1),   # two-level split tree
     (1, "split_grid", 1),
     (2, "split_grid", 2),    # on MANY_UNITS: split kernel + combine kernel
+    (0, "split_grid_paired", 1),  # on PAIRED: two KV heads per workgroup, two-level tree
 ])
 @pytest.mark.parametrize("sq,causal", [(1, False), (4, True)])
 def test_captured_decode_replays_to_the_eager_result(num_splits, schedule, launches, sq, causal):
@@ -51,6 +55,8 @@ def test_captured_decode_replays_to_the_eager_result(num_splits, schedule, launc
     Hq, Hkv, D = 32, 8, 128
     if launches == 2:
         lens, Hq, D = MANY_UNITS, 16, 64
+    if schedule == "split_grid_paired":
+        lens, sq = PAIRED, min(sq, 2)   # pairs hold 2 * seqlen_q * group <= 16 rows
     inp = _inputs(lens, Hq, Hkv, D, 16, sq=sq, seed=num_splits + sq)
     ws, p = _workspace(inp, num_splits)
     assert p["schedule"] == schedule and p["launches"] == launches

@@ -603,6 +603,85 @@ def test_split_grid_with_more_units_than_counters_uses_the_combine_kernel():
 
 
 # ------------------------------------------------------------------------------------------
+# Paired split grid: two adjacent KV heads per workgroup, two waves per head
+# ------------------------------------------------------------------------------------------
+
+PAIR_LENS = [0, 1, 17, 1025, 9000, 16384]
+
+
+def _paired_inputs(sq=1, seed=0, lens=PAIR_LENS, Hq=32, Hkv=8, P=16):
+    spec = W.custom_spec("pair", lens, Hq, Hkv, 128, P, max_pages=16384 // P, seqlen_q=sq)
+    return W.make_inputs(spec, seed=seed, device=DEV)
+
+
+@pytest.mark.parametrize("Hq,Hkv,P", [(32, 8, 16), (32, 8, 64), (64, 8, 16)])
+def test_paired_split_grid_matches_oracle(Hq, Hkv, P):
+    """The automatic plan pairs heads on these shapes; every sequence (empty, one token, a
+    page boundary plus one, a chunk past a split, long) against the oracle; repeated calls are
+    identical (the merge counters reset themselves) and the device status stays clean."""
+    from mx_flash_attn_kernel_opt__amd import plan
+    inp = _paired_inputs(Hq=Hq, Hkv=Hkv, P=P, seed=Hq + P)
+    s = inp.spec
+    p = plan(s.batch, Hq, Hkv, 128, P, s.max_pages)
+    assert p["schedule"] == "split_grid_paired" and p["launches"] == 1
+    out = _decode(inp).clone()
+    _check(inp, out, label=f"paired Hq={Hq} Hkv={Hkv} P={P}")
+    assert not out[0].float().abs().any().item()          # the empty sequence
+    assert torch.equal(_decode(inp), out)
+    assert read_device_status() == 0
+
+
+def test_paired_split_grid_matches_unpaired():
+    """Paired (automatic) against one head per workgroup (an explicit split count, which is
+    never paired): the same rows to within the tolerance."""
+    inp = _paired_inputs(seed=5)
+    paired = _decode(inp).float()
+    single = _decode(inp, num_splits=21).float()
+    assert (paired - single).abs().max().item() <= 1e-2
+
+
+@pytest.mark.parametrize("sq", [1, 2])
+def test_paired_split_grid_causal_and_multi_token(sq):
+    """2 query tokens x group 4 x 2 heads = 16 rows: the largest paired tile, causal."""
+    from mx_flash_attn_kernel_opt__amd import plan
+    inp = _paired_inputs(sq=sq, seed=9 + sq)
+    s = inp.spec
+    assert plan(s.batch, 32, 8, 128, 16, s.max_pages, seqlen_q=sq)["schedule"] == \
+        "split_grid_paired"
+    out = _decode(inp, causal=True)
+    _mq_check(inp, out, True, f"paired causal sq={sq}")
+
+
+def test_paired_split_grid_two_phase_combine():
+    """MX_PHASE_MAIN_ONLY then MX_PHASE_COMBINE_ONLY on the paired plan: the combine kernel
+    reads the paired partials (the stored rows, splits innermost)."""
+    from mx_flash_attn_kernel_opt__amd import _lib
+    inp = _paired_inputs(seed=13)
+    fused = _decode(inp).clone()
+    two = torch.empty_like(fused)
+    for phase in (_lib.MX_PHASE_MAIN_ONLY, _lib.MX_PHASE_COMBINE_ONLY):
+        paged_gqa_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_table, inp.seq_lens,
+                         inp.scale, out=two, phase=phase)
+    torch.cuda.synchronize()
+    _check(inp, two, label="paired two-phase")
+    assert (fused.float() - two.float()).abs().max().item() <= 1e-2
+
+
+def test_paired_split_grid_partial_outputs():
+    """mx_paged_gqa_decode_partial on the paired plan: fp32 rows and natural-log lse of both
+    heads of every pair against the unsharded oracle."""
+    from mx_flash_attn_kernel_opt__amd import paged_gqa_decode_partial
+    inp = _paired_inputs(seed=17)
+    o, lse = paged_gqa_decode_partial(inp.q, inp.k_cache, inp.v_cache, inp.block_table,
+                                      inp.seq_lens, inp.scale)
+    torch.cuda.synchronize()
+    ref = paged_decode_reference(inp.q.cpu(), inp.k_cache.cpu(), inp.v_cache.cpu(),
+                                 inp.block_table.cpu(), inp.seq_lens.cpu(), inp.scale)
+    assert_close_to_oracle(o.cpu().to(torch.bfloat16), ref, "paired partial o")
+    assert torch.isneginf(lse[0]).all().item() and torch.isfinite(lse[1:]).all().item()
+
+
+# ------------------------------------------------------------------------------------------
 # Query groups above 16 (MQA-style: up to 128 query heads per KV head)
 # ------------------------------------------------------------------------------------------
 

@@ -210,11 +210,12 @@ def test_balanced_plan(B, Hq, Hkv, D, ns_req, groups):
 def test_policy_on_the_north_star_configs():
     """The automatic plan on a 256-CU MI355X (from interleaved A/B sweeps): batches of at
     least 64 (sequence, KV head) units take the balanced single launch; fewer, long units take
-    the split grid with about one workgroup per CU."""
+    the split grid with about one workgroup per CU, over pairs of KV heads where each paired
+    split keeps at least 1 024 tokens."""
     expect = {
         "tiny": ("split_grid", 4), "llama3_8b": ("balanced", 256),
-        "long_b1_32k": ("split_grid", 32), "long_b1_128k": ("split_grid", 32),
-        "long_b4_32k": ("split_grid", 8), "long_b4_128k": ("split_grid", 8),
+        "long_b1_32k": ("split_grid", 32), "long_b1_128k": ("split_grid_paired", 64),
+        "long_b4_32k": ("split_grid_paired", 16), "long_b4_128k": ("split_grid_paired", 16),
         "ragged": ("balanced", 256), "sweep_b32_16k": ("balanced", 256),
         "sweep_b128_16k": ("balanced", 256), "sweep_d64": ("balanced", 512),
         "sweep_d256": ("balanced", 256),
@@ -225,6 +226,36 @@ def test_policy_on_the_north_star_configs():
         sched, n = expect[name]
         assert p["schedule"] == sched, name
         assert (p["workgroups"] if sched == "balanced" else p["splits"]) == n, name
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,cap,sq,fp8,ns_req,sched,splits", [
+    (1, 64, 8, 128, 131072, 1, False, 0, "split_grid_paired", 64),
+    (4, 64, 8, 128, 32768, 1, False, 0, "split_grid_paired", 16),
+    (1, 64, 8, 128, 32768, 1, False, 0, "split_grid", 32),    # paired splits of 512 tokens
+    (1, 64, 8, 128, 131072, 1, True, 0, "split_grid", 32),    # fp8 caches are not paired
+    (1, 64, 8, 128, 131072, 1, False, 32, "split_grid", 32),  # explicit split counts are not
+    (1, 56, 7, 128, 131072, 1, False, 0, "split_grid", 37),   # odd KV head count
+    (1, 64, 4, 128, 131072, 1, False, 0, "split_grid", 64),   # group 16: 32 rows per pair
+    (1, 32, 8, 128, 131072, 2, False, 0, "split_grid_paired", 64),  # 2 tokens x group 4
+    (1, 32, 8, 128, 131072, 3, False, 0, "split_grid", 32),   # 3 x 4 x 2 = 24 rows
+    (1, 32, 8, 64, 131072, 1, False, 0, "split_grid", 64),    # head_dim 64
+    (1, 16, 4, 256, 131072, 1, False, 0, "split_grid", 64),   # head_dim 256
+])
+def test_paired_split_grid_plan(B, Hq, Hkv, D, cap, sq, fp8, ns_req, sched, splits):
+    """Pairs of adjacent KV heads share a workgroup on the automatic split grid (bf16 cache,
+    head_dim 128, an even KV head count, 2 * seqlen_q * group <= 16, paired splits of at least
+    1 024 tokens): units of two heads, about one workgroup per CU, the same partial rows."""
+    p = plan(B, Hq, Hkv, D, 16, cap // 16, 0, ns_req, num_cus=256, seqlen_q=sq, fp8=fp8)
+    assert p["schedule"] == sched and p["splits"] == splits
+    units = B * (Hkv // 2 if sched == "split_grid_paired" else Hkv)
+    row_groups = 1 if sched == "split_grid_paired" else math.ceil(sq * Hq // Hkv / 16 / (
+        2 if sq * Hq // Hkv > 16 and D <= 128 else 1))
+    assert p["workgroups"] == units * row_groups * splits
+    prow = B * sq * Hq * splits
+    assert p["workspace_bytes"] == PARTIAL_BASE + math.ceil(prow * 4 / 256) * 256 + prow * D * 4
+    assert p["launches"] == 1
+    if sched == "split_grid_paired":
+        assert p["tokens_per_split"] >= 1024
 
 
 @pytest.mark.parametrize("B,Hkv,cap,sched,splits", [
@@ -428,7 +459,7 @@ def test_balanced_schedule_bounds_its_32_bit_chunk_line():
     capacity chunks reach 2^30 take the split grid, and forcing the balanced schedule fails."""
     # 512 x 16 units of 4M tokens (262 144 chunks each): 2^31 chunks of capacity
     p = plan(512, 16, 16, 128, 256, 16384, 0, 0, num_cus=256)
-    assert p["schedule"] == "split_grid"
+    assert p["schedule"] == "split_grid_paired"  # a split grid, over pairs of heads
     with pytest.raises(MXAttnError) as e:
         plan(512, 16, 16, 128, 256, 16384, 0, -10, num_cus=256)
     assert e.value.status == _lib.MX_STATUS_UNSUPPORTED
