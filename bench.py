@@ -355,7 +355,7 @@ def time_launch_ab(inp: W.DecodeInputs, steps: int, warmup: int) -> dict:
                                             for _ in range(copies - 1)]
     plan = pkg.plan(spec.batch, spec.num_heads, spec.num_kv_heads, spec.head_dim,
                     spec.page_size, spec.max_pages, 0, 0, seqlen_q=spec.seqlen_q)
-    if plan["schedule"] == "balanced" or plan["splits"] < 2:
+    if plan["schedule"].startswith("balanced") or plan["splits"] < 2:
         raise ValueError(f"{spec.name}: the automatic plan is not a split grid with splits")
     ws = pkg.make_workspace(plan["workspace_bytes"], inp.device)
     out = torch.empty_like(inp.q)
@@ -609,14 +609,14 @@ def result_line(args, spec, r, cpu=None) -> dict:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": ("mx_paged_decode_balanced" if r["plan"]["schedule"] == "balanced"
+            "kernel": ("mx_paged_decode_balanced" if r["plan"]["schedule"].startswith("balanced")
                        else "mx_paged_decode_splitkv"),
             "achieved": round(r["kernel_gbps"], 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(frac, 4),
             "traffic": _traffic_from_profile(
-                "balanced" if r["plan"]["schedule"] == "balanced" else "splitkv",
+                "balanced" if r["plan"]["schedule"].startswith("balanced") else "splitkv",
                 spec.name + ("_fp8" if r["fp8"] else "")),
             "kernel_us_mean": round(r["kernel_us_mean"], 2),
             # "step": the call is this one kernel, timed back to back over the timed region;

@@ -64,9 +64,12 @@ extern "C" {
                                       batch's K/V chunks evenly from seq_lens on the device and
                                       merge split sequences themselves                            */
 #define MX_SCHEDULE_SPLIT_GRID_PAIRED 2 /* the split grid over pairs of adjacent KV heads, two
-                                      waves of each workgroup per head (automatic splits of
-                                      >= 1024 tokens, head_dim 128, bf16 cache, no fused
-                                      append, 2 * seqlen_q * group <= 16)                         */
+                                      waves of each workgroup per head: automatic plans of
+                                      bf16 decodes without a fused append, head_dim 128, an
+                                      even num_kv_heads >= 8, 2 * seqlen_q * group <= 16, and
+                                      splits of >= 1024 tokens                                    */
+#define MX_SCHEDULE_BALANCED_PAIRED 3 /* the balanced schedule over pairs of adjacent KV heads,
+                                      on the same shapes as MX_SCHEDULE_SPLIT_GRID_PAIRED       */
 
 /* Phase flags for mx_paged_gqa_decode (0 = run everything). */
 #define MX_PHASE_MAIN_ONLY 1        /* split grid: run only the split-KV kernel, partials stay in

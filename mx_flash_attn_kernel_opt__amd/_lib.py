@@ -30,6 +30,7 @@ MX_DEVICE_SEQ_TOO_LONG = 2
 MX_SCHEDULE_SPLIT_GRID = 0
 MX_SCHEDULE_BALANCED = 1
 MX_SCHEDULE_SPLIT_GRID_PAIRED = 2
+MX_SCHEDULE_BALANCED_PAIRED = 3
 
 MX_PHASE_ALL = 0
 MX_PHASE_MAIN_ONLY = 1

@@ -1688,7 +1688,12 @@ struct BalancedTree {
 // entirely is written out as bf16; a unit cut into several pieces has each piece written as
 // a normalised partial (O/l, log2-sum-exp) to its own slot, and the last piece to finish
 // merges them through a fan-in-8 tree of per-unit counters, so the whole call is one launch.
-template <int D, int NBUF, int NW, bool kCausal, int KT, bool kAppend, bool kFp8>
+//
+// kPairW (MX_SCHEDULE_BALANCED_PAIRED): units are (sequence, pair of adjacent KV heads), streamed
+// as in mx_paged_decode_splitkv with kPairW (waves 0-1 the first head, 2-3 the second), and a
+// pair's chunk weighs twice a single head's on the line (MainShape::chunk_weight).
+template <int D, int NBUF, int NW, bool kCausal, int KT, bool kAppend, bool kFp8,
+          bool kPairW = false>
 __global__ __launch_bounds__(64 * NW)
 __attribute__((amdgpu_waves_per_eu(min_waves_per_simd<D, KT>())))
 void mx_paged_decode_balanced(
@@ -1874,6 +1879,11 @@ void mx_paged_decode_balanced(
         stream_chunks<D, NBUF, NW, kCausal, KT, NewTokens<kFp8>, kFp8>(st, qop, kc, vc, bt_row, kv, ca, c_end,
                                                 ext.cache, c_mask, row_lim, wv,
                                                 L::ktile(lds, wv), sh, bad_page, nt);
+      } else if constexpr (kPairW) {
+        static_assert(NW == 4 && KT == 1 && !kAppend, "paired waves: four waves, one row tile");
+        stream_chunks<D, NBUF, 2, kCausal, KT, NoExtraChunk, kFp8>(
+            st, qop, kc, vc, bt_row, 2 * kv + (wv >> 1), ca, c_end, ext.cache, c_mask, row_lim,
+            wv & 1, L::ktile(lds, wv), sh, bad_page);
       } else {
         stream_chunks<D, NBUF, NW, kCausal, KT, NoExtraChunk, kFp8>(
             st, qop, kc, vc, bt_row, kv, ca, c_end, ext.cache, c_mask, row_lim, wv,
@@ -1888,7 +1898,11 @@ void mx_paged_decode_balanced(
           const int hh = e / (D / 4);
           const int d = 4 * (e - hh * (D / 4));
           float lse;
-          const f32x4 o = merged_head<D, NW, KT>(lds, hh, d, lse);
+          f32x4 o;
+          if constexpr (kPairW)
+            o = merged_head_pair<D>(lds, hh, d, lse, sh);
+          else
+            o = merged_head<D, NW, KT>(lds, hh, d, lse);
           store_row4<D>(out, sh, rbase + row_offset(r0 + hh, sh), d, o, lse);
         }
       } else {
@@ -1902,7 +1916,12 @@ void mx_paged_decode_balanced(
             const int hh = e / (D / 4);
             const int d = 4 * (e - hh * (D / 4));
             float lse;
-            store_partial4(po + hh * D + d, merged_head<D, NW, KT>(lds, hh, d, lse));
+            f32x4 o;
+            if constexpr (kPairW)
+              o = merged_head_pair<D>(lds, hh, d, lse, sh);
+            else
+              o = merged_head<D, NW, KT>(lds, hh, d, lse);
+            store_partial4(po + hh * D + d, o);
             if (d == 0) store_partial1(pl + hh, lse);
           }
         }
@@ -2263,9 +2282,12 @@ struct Plan {
   int chunk_shift = 0;
 };
 
-// KV heads of the kernels' units: pairs of the (kernel) heads on the paired split grid.
+// KV heads of the kernels' units: pairs of the (kernel) heads on the paired schedules.
 int64_t plan_kv_heads(const Plan& plan, int64_t kv_heads) {
-  return plan.schedule == MX_SCHEDULE_SPLIT_GRID_PAIRED ? kv_heads / 2 : kv_heads;
+  return (plan.schedule == MX_SCHEDULE_SPLIT_GRID_PAIRED ||
+          plan.schedule == MX_SCHEDULE_BALANCED_PAIRED)
+             ? kv_heads / 2
+             : kv_heads;
 }
 
 int query_num_cus(int64_t* num_cus) {
@@ -2292,6 +2314,16 @@ int query_num_cus(int64_t* num_cus) {
 }
 
 // Validates the shape and computes the split plan.  Performs no HIP call when num_cus > 0.
+// Whether an automatic plan runs adjacent KV heads in pairs, two waves per head
+// (MX_SCHEDULE_SPLIT_GRID_PAIRED, MX_SCHEDULE_BALANCED_PAIRED): bf16 decodes without a fused
+// append (pair_ok), head_dim 128, token rows of at least 2 KB (>= 8 KV heads, an even count) and
+// both heads' rows in one 16-row tile.
+bool pair_heads(bool pair_ok, int64_t num_splits, int64_t head_dim, int64_t num_kv_heads,
+                int64_t rows) {
+  return pair_ok && num_splits == 0 && head_dim == 128 && num_kv_heads % 2 == 0 &&
+         num_kv_heads * head_dim * 2 >= 2048 && 2 * rows <= 16;
+}
+
 // Automatic split count of the split grid: enough splits for `slots` resident workgroups over
 // `units` units, each split holding at least kMinTokensPerSplit tokens at capacity `cap` (and
 // splitting starts at four splits: the partial round trip and merge, ~3.5 us, are only repaid
@@ -2401,12 +2433,26 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
     plan->splits = 0;
     plan->tokens_per_split = 0;
     plan->groups = groups;
-    plan->slots = groups + units;
+    int64_t line_units = units;
+    int64_t slot_rows = tile_rows;
+    // Paired heads (MX_SCHEDULE_BALANCED_PAIRED): interleaved A/B against one head per unit,
+    // sweep B=32 16K 331.9 against 344.9 us, B=128 16K 1294.5 against 1307.6, group 1 on config
+    // 2's bytes 164.8 against 167.6, config 2 159.2/165.9 against 161.0/165.9 (two runs);
+    // ragged lengths with 8 KV heads (B=256, G=4, P=64) 143.0 against 148.5.  With 4 KV heads
+    // (1 KB token rows) pairing gained nothing (ragged P=16 82.2 against 81.9, uniform 165.4
+    // against 165.9) or lost (config 4, P=64: 84.3 against 80.1), so it needs 2 KB token rows.
+    if (pair_heads(pair_ok, num_splits, head_dim, num_kv_heads, rows)) {
+      plan->schedule = MX_SCHEDULE_BALANCED_PAIRED;
+      plan->rows = 2 * rows;
+      line_units = units / 2;
+      slot_rows = 2 * rows;
+    }
+    plan->slots = groups + line_units;
     plan->cap_tokens = cap;
     plan->counter_offset = kStatusBytes;
     plan->lse_offset = kPartialBase;
-    plan->o_offset = plan->lse_offset + align_up(plan->slots * tile_rows * 4, 256);
-    plan->workspace_bytes = plan->o_offset + plan->slots * tile_rows * head_dim * 4;
+    plan->o_offset = plan->lse_offset + align_up(plan->slots * slot_rows * 4, 256);
+    plan->workspace_bytes = plan->o_offset + plan->slots * slot_rows * head_dim * 4;
     return MX_STATUS_OK;
   }
   if (num_splits < 0)
@@ -2422,8 +2468,7 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
   // B=4 128K 329.7 against 349.1 us, B=1 128K 91.5 against 94.5, B=4 32K 90.5 against 92.5.
   // Shorter splits lose: B=1 at 32K (512 tokens per paired split) 31.1 against 30.0 us, where
   // the tree's partials of 16 rows lengthen the merge tail.
-  if (pair_ok && num_splits == 0 && head_dim == 128 && num_kv_heads % 2 == 0 &&
-      2 * rows <= 16) {
+  if (pair_heads(pair_ok, num_splits, head_dim, num_kv_heads, rows)) {
     int64_t ns2 = auto_splits(batch * (num_kv_heads / 2), num_cus * groups_per_cu(head_dim), cap);
     if (ns2 > cap_pages) ns2 = cap_pages;
     if (ns2 < 1) ns2 = 1;
@@ -2563,8 +2608,9 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   constexpr int kNBUF = ring_depth<D>();
   constexpr int kNBUF8 = ring_depth_fp8<D>();
   MainShape sh;
-  // Strides are the stored heads'; the paired split grid's kernel heads are pairs of them.
-  const bool paired = plan.schedule == MX_SCHEDULE_SPLIT_GRID_PAIRED;
+  // Strides are the stored heads'; the paired schedules' kernel heads are pairs of them.
+  const bool paired = plan.schedule == MX_SCHEDULE_SPLIT_GRID_PAIRED ||
+                      plan.schedule == MX_SCHEDULE_BALANCED_PAIRED;
   const int64_t kernel_kv = plan_kv_heads(plan, num_kv_heads);
   sh.page_stride = page_size * num_kv_heads * D;
   sh.token_stride = (int)(num_kv_heads * D);
@@ -2592,7 +2638,8 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   sh.split_groups = 1;
   sh.tokens_per_split = (int)plan.tokens_per_split;
   sh.num_groups = (int)plan.groups;
-  sh.chunk_weight = kChunkPositions;
+  // A paired unit's chunk holds two heads' rows: twice a single head's weight on the line.
+  sh.chunk_weight = paired ? 2 * kChunkPositions : kChunkPositions;
   sh.unit_overhead = kUnitOverhead;
   sh.num_slots = (int)plan.slots;
   sh.o_out = o_out;
@@ -2612,7 +2659,7 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   const uint8_t* k8 = static_cast<const uint8_t*>(k);
   const uint8_t* v8 = static_cast<const uint8_t*>(v);
 
-  if (plan.schedule == MX_SCHEDULE_BALANCED) {
+  if (plan.schedule == MX_SCHEDULE_BALANCED || plan.schedule == MX_SCHEDULE_BALANCED_PAIRED) {
     // One launch does everything; MX_PHASE_COMBINE_ONLY has nothing left to do.
     if (phase == MX_PHASE_COMBINE_ONLY) return hipSuccess;
     auto go = [&](auto kernel, auto kc, auto vc) {
@@ -2622,7 +2669,15 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
                          reinterpret_cast<float*>(ws + plan.lse_offset),
                          reinterpret_cast<uint32_t*>(ws + plan.counter_offset), status, sh);
     };
-    if (kv.fp8 && append)
+    if (paired) {
+      // make_plan pairs only bf16 decodes without a fused append, at head_dim 128, one tile.
+      if constexpr (D == 128 && KT == 1) {
+        if (kv.fp8 || append) return hipErrorInvalidValue;
+        go(mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, false, false, true>, k16, v16);
+      } else {
+        return hipErrorInvalidValue;
+      }
+    } else if (kv.fp8 && append)
       go(mx_paged_decode_balanced<D, kNBUF8, kNW, kCausal, KT, true, true>, k8, v8);
     else if (kv.fp8)
       go(mx_paged_decode_balanced<D, kNBUF8, kNW, kCausal, KT, false, true>, k8, v8);
@@ -2704,7 +2759,8 @@ static int report_plan(bool fp8, int64_t batch, int64_t seqlen_q, int64_t num_he
   if (splits_out) *splits_out = plan.splits;
   if (tokens_per_split_out) *tokens_per_split_out = plan.tokens_per_split;
   if (workgroups_out)
-    *workgroups_out = plan.schedule == MX_SCHEDULE_BALANCED
+    *workgroups_out = (plan.schedule == MX_SCHEDULE_BALANCED ||
+                       plan.schedule == MX_SCHEDULE_BALANCED_PAIRED)
                           ? plan.groups
                           : batch * plan_kv_heads(plan, kh.kv_heads) * plan.row_tiles * plan.splits;
   if (workspace_bytes_out) *workspace_bytes_out = plan.workspace_bytes;

@@ -44,8 +44,8 @@ def plan(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, page_size
     (e4m3fn) cache.
 
     Returns ``{"schedule", "splits", "tokens_per_split", "workgroups", "workspace_bytes",
-    "launches"}`` (schedule: "split_grid", "split_grid_paired" or "balanced"; launches: kernels a
-    phase-0 call runs);
+    "launches"}`` (schedule: "split_grid", "balanced", or either with "_paired": adjacent KV
+    heads in pairs; launches: kernels a phase-0 call runs);
     raises MXAttnError for an invalid or unsupported shape.
     """
     lib = _lib.load()
@@ -56,14 +56,15 @@ def plan(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, page_size
                ctypes.byref(tps), ctypes.byref(wgs), ctypes.byref(ws))
     _lib.check(st)
     schedule = {_lib.MX_SCHEDULE_SPLIT_GRID: "split_grid", _lib.MX_SCHEDULE_BALANCED: "balanced",
-                _lib.MX_SCHEDULE_SPLIT_GRID_PAIRED: "split_grid_paired"}[sch.value]
+                _lib.MX_SCHEDULE_SPLIT_GRID_PAIRED: "split_grid_paired",
+                _lib.MX_SCHEDULE_BALANCED_PAIRED: "balanced_paired"}[sch.value]
     # Launches of a phase-0 call: the balanced schedule and the split grid with one split are
     # one launch; the split grid merges its splits through an in-kernel tree when there are at
     # most MAX_MERGE_ITEMS and every unit's ceil(splits / MERGE_FAN_IN) arrival counters fit the
     # counter region, else a combine kernel follows (csrc/paged_decode.hip, split_tree_fits).
     # The split grid launches units x splits workgroups.
     units = wgs.value // max(ns.value, 1)
-    two = (schedule != "balanced" and ns.value > 1 and
+    two = (schedule.startswith("split_grid") and ns.value > 1 and
            (ns.value > MAX_MERGE_ITEMS or
             units * math.ceil(ns.value / MERGE_FAN_IN) > COUNTER_SLOTS))
     return {"schedule": schedule, "splits": ns.value, "tokens_per_split": tps.value,

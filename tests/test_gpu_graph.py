@@ -42,7 +42,7 @@ PAIRED = [0, 1, 17, 1025, 9000, 16384]            # few long units: the paired s
 
 
 @pytest.mark.parametrize("num_splits,schedule,launches", [
-    (0, "balanced", 1),      # merge tree with arrival counters reset in-kernel
+    (0, "balanced", 1),      # merge tree with arrival counters reset in-kernel (sq=1: paired)
     (4, "split_grid", 1),    # one-level split tree (arrival counters reset by it)
     (32, "split_grid", 1),   # two-level split tree
     (1, "split_grid", 1),
@@ -59,7 +59,10 @@ def test_captured_decode_replays_to_the_eager_result(num_splits, schedule, launc
         lens, sq = PAIRED, min(sq, 2)   # pairs hold 2 * seqlen_q * group <= 16 rows
     inp = _inputs(lens, Hq, Hkv, D, 16, sq=sq, seed=num_splits + sq)
     ws, p = _workspace(inp, num_splits)
-    assert p["schedule"] == schedule and p["launches"] == launches
+    assert p["launches"] == launches
+    # Adjacent KV heads run in pairs where both heads' rows fit one 16-row tile.
+    assert p["schedule"] == (schedule + "_paired" if schedule == "balanced" and sq == 1
+                             else schedule)
     out = torch.empty_like(inp.q)
     kw = dict(out=out, causal=causal, num_splits=num_splits, workspace=ws)
 

@@ -631,6 +631,27 @@ def test_paired_split_grid_matches_oracle(Hq, Hkv, P):
     assert read_device_status() == 0
 
 
+@pytest.mark.parametrize("P", [16, 64])
+@pytest.mark.parametrize("sq,causal", [(1, False), (2, True)])
+def test_paired_balanced_ragged(P, sq, causal):
+    """The balanced schedule over pairs of KV heads: a ragged batch with empty, one-token,
+    page-boundary and long sequences (units whole, cut into pieces and merged), against the
+    oracle; repeated calls are identical and the device status stays clean."""
+    from mx_flash_attn_kernel_opt__amd import plan
+    g = torch.Generator().manual_seed(P + sq)
+    lens = [0, 1, 15, 16, 17, 64, 1000, 4096, 8191] + \
+        torch.randint(1, 8192, (39,), generator=g).tolist()
+    spec = W.custom_spec("pairbal", lens, 32, 8, 128, P, max_pages=8192 // P, seqlen_q=sq)
+    inp = W.make_inputs(spec, seed=P * sq, device=DEV)
+    assert plan(spec.batch, 32, 8, 128, P, spec.max_pages, seqlen_q=sq)["schedule"] == \
+        "balanced_paired"
+    out = _decode(inp, causal=causal).clone()
+    _mq_check(inp, out, causal, f"paired balanced P={P} sq={sq}")
+    assert not out[0].float().abs().any().item()          # the empty sequence
+    assert torch.equal(_decode(inp, causal=causal), out)
+    assert read_device_status() == 0
+
+
 def test_paired_split_grid_matches_unpaired():
     """Paired (automatic) against one head per workgroup (an explicit split count, which is
     never paired): the same rows to within the tolerance."""

@@ -92,7 +92,7 @@ def _ragged(B, lo, hi, seed):
 
 @pytest.mark.parametrize("num_shards", [1, 4])
 @pytest.mark.parametrize("num_splits,expect", [
-    (0, "balanced"),        # automatic: 128 units -> balanced; long units -> merge tree
+    (0, "balanced_paired"),  # automatic: 128 units -> balanced over pairs of KV heads
     (1, "split_grid"),      # one split per sequence: the main kernel writes the rows
     (4, "split_grid"),      # in-kernel merge by the last split (one shard: up to 4 splits)
     (32, "split_grid"),     # one shard: 32 splits, a two-level in-kernel tree writes the rows;

@@ -189,20 +189,23 @@ def test_split_grid_plan_invariants(B, Hq, Hkv, D, P, max_pages, cap, ns_req):
         assert ws == PARTIAL_BASE + math.ceil(rows * 4 / 256) * 256 + rows * D * 4
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,D,ns_req,groups", [
-    (64, 32, 8, 128, 0, 256),      # automatic: one 4-wave workgroup per CU at D=128
-    (128, 32, 4, 64, 0, 512),      # two 2-wave workgroups per CU at D=64
-    (64, 16, 2, 256, 0, 256),      # one per CU at D=256
-    (4, 32, 8, 128, -7, 7),        # forced workgroup count
-    (512, 28, 4, 128, 0, 256),
-    (3, 32, 8, 128, -9000, 4095),  # clamped to the 8^4 merge tree
+@pytest.mark.parametrize("B,Hq,Hkv,D,ns_req,groups,paired", [
+    (64, 32, 8, 128, 0, 256, True),      # automatic: one 4-wave workgroup per CU at D=128
+    (128, 32, 4, 64, 0, 512, False),     # two 2-wave workgroups per CU at D=64
+    (64, 16, 2, 256, 0, 256, False),     # one per CU at D=256
+    (4, 32, 8, 128, -7, 7, False),       # forced workgroup count: never paired
+    (512, 28, 4, 128, 0, 256, False),    # 4 KV heads: 1 KB token rows are not paired
+    (3, 32, 8, 128, -9000, 4095, False),  # clamped to the 8^4 merge tree
+    (32, 128, 16, 128, 0, 256, True),    # 16 KV heads, group 8: pairs of 16 rows
 ])
-def test_balanced_plan(B, Hq, Hkv, D, ns_req, groups):
+def test_balanced_plan(B, Hq, Hkv, D, ns_req, groups, paired):
+    """Slots of the balanced schedule: one per workgroup and one per unit, of min(rows, 16)
+    rows; paired units are two adjacent KV heads with both heads' rows."""
     p = plan(B, Hq, Hkv, D, 16, 256, 0, ns_req, num_cus=256)
-    assert p["schedule"] == "balanced"
+    assert p["schedule"] == ("balanced_paired" if paired else "balanced")
     assert p["workgroups"] == groups and p["splits"] == 0
-    slots = groups + B * Hkv
-    G = Hq // Hkv
+    slots = groups + B * Hkv // (2 if paired else 1)
+    G = Hq // Hkv * (2 if paired else 1)
     o_off = PARTIAL_BASE + math.ceil(slots * G * 4 / 256) * 256
     assert p["workspace_bytes"] == o_off + slots * G * D * 4
 
@@ -213,11 +216,11 @@ def test_policy_on_the_north_star_configs():
     the split grid with about one workgroup per CU, over pairs of KV heads where each paired
     split keeps at least 1 024 tokens."""
     expect = {
-        "tiny": ("split_grid", 4), "llama3_8b": ("balanced", 256),
+        "tiny": ("split_grid", 4), "llama3_8b": ("balanced_paired", 256),
         "long_b1_32k": ("split_grid", 32), "long_b1_128k": ("split_grid_paired", 64),
         "long_b4_32k": ("split_grid_paired", 16), "long_b4_128k": ("split_grid_paired", 16),
-        "ragged": ("balanced", 256), "sweep_b32_16k": ("balanced", 256),
-        "sweep_b128_16k": ("balanced", 256), "sweep_d64": ("balanced", 512),
+        "ragged": ("balanced", 256), "sweep_b32_16k": ("balanced_paired", 256),
+        "sweep_b128_16k": ("balanced_paired", 256), "sweep_d64": ("balanced", 512),
         "sweep_d256": ("balanced", 256),
     }
     for name, s in W.NORTH_STAR.items():
@@ -225,7 +228,7 @@ def test_policy_on_the_north_star_configs():
                  num_cus=256)
         sched, n = expect[name]
         assert p["schedule"] == sched, name
-        assert (p["workgroups"] if sched == "balanced" else p["splits"]) == n, name
+        assert (p["workgroups"] if sched.startswith("balanced") else p["splits"]) == n, name
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,D,cap,sq,fp8,ns_req,sched,splits", [
@@ -264,8 +267,8 @@ def test_paired_split_grid_plan(B, Hq, Hkv, D, cap, sq, fp8, ns_req, sched, spli
     (16, 4, 141, "split_grid", 1),      # 141 tokens: a second split would hold < 128
     (16, 4, 512, "split_grid", 4),      # 64 units: four 128-token splits fill the CUs
     (64, 4, 1024, "split_grid", 1),     # 1 024 tokens with 256 units: split grid
-    (64, 8, 1024, "balanced", 0),       # ... with 512 units: balanced
-    (16, 8, 2048, "balanced", 0),       # from 2 048 tokens: balanced
+    (64, 8, 1024, "balanced_paired", 0),  # ... with 512 units: balanced (8 heads: paired)
+    (16, 8, 2048, "balanced_paired", 0),  # from 2 048 tokens: balanced
 ])
 def test_policy_capacity_gate(B, Hkv, cap, sched, splits):
     """Batches of short sequences skip the balanced schedule (its length scan and merges cost
@@ -464,7 +467,8 @@ def test_balanced_schedule_bounds_its_32_bit_chunk_line():
         plan(512, 16, 16, 128, 256, 16384, 0, -10, num_cus=256)
     assert e.value.status == _lib.MX_STATUS_UNSUPPORTED
     # the same batch with a 64K-token capacity stays balanced
-    assert plan(512, 16, 16, 128, 256, 16384, 65536, 0, num_cus=256)["schedule"] == "balanced"
+    assert plan(512, 16, 16, 128, 256, 16384, 65536, 0,
+                num_cus=256)["schedule"] == "balanced_paired"
 
 
 # ------------------------------------------------------------------------------------------
