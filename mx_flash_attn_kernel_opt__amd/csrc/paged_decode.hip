@@ -1402,7 +1402,7 @@ __device__ __forceinline__ void merge_elems(const Tree& tree, int e0, int total,
 
 // The whole step: nrows * D/4 elements over the workgroup's 64*NW threads, two per thread and
 // round when there are more elements than threads (16 rows at D=128 take one round instead of
-// two: two round trips per level lengthened the tail of paired-head split grids by ~2 us).
+// two; paired split grid at B=1, 32K tokens: 31.1 against 32.4 us per call with two rounds).
 template <int D, int NW, int W, class Tree>
 __device__ __forceinline__ void merge_group(const Tree& tree, int gslot, int stride, int gsize,
                                             int nrows, bool final, float* s_lse) {

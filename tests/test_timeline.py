@@ -1,5 +1,6 @@
-"""The per-workgroup timeline tool's host side: the summary of one launch's stamp table, and the
-timeline build's line costings (no GPU, no compilation)."""
+"""Host side of the measurement tools: the per-workgroup timeline's summary of one launch's
+stamp table, the timeline build's line costings, and the head-row probe's per-head finish
+times (no GPU, no compilation)."""
 
 from __future__ import annotations
 
@@ -60,3 +61,15 @@ def test_line_costings_are_powers_of_two_per_chunk():
         assert per_unit >= 0
         assert T.lib_path(tag).endswith(f"libmxattn_timeline_{tag}.so")
     assert T.LINE_COSTS["line8"] == (8, 64)    # the shipped costing
+
+
+def test_row_probe_head_end_times():
+    """The head-row probe's summary: workgroup w serves unit w % units; a pair unit's end is
+    both of its heads' end."""
+    from mx_flash_attn_kernel_opt__amd import row_probe as R
+    # 2 heads single: units 0, 1, shares 2 -> workgroups 0 (head 0), 1 (head 1), 2 (head 0), ...
+    stamps = [(100, 500), (120, 900), (110, 700), (130, 600)]
+    assert R.head_end_times(stamps, 2, False, 2) == [6.0, 8.0]
+    # 4 heads paired: units (0,1), (2,3)
+    stamps = [(100, 400), (100, 800), (100, 300), (150, 650)]
+    assert R.head_end_times(stamps, 4, True, 2) == [3.0, 3.0, 7.0, 7.0]
