@@ -1120,7 +1120,9 @@ struct NewTokens {
     constexpr int RPI = 64 / SPR;  // K rows per load instruction
     constexpr int VW = D / 16;     // V elements per lane and row
     const int S = sh.new_tokens;
-    const int64_t head0 = ((int64_t)b * S * sh.num_kv_heads + kv) * D;  // row 0 of head kv
+    // Row 0 of stored head kv: k_new / v_new rows have the cache's token stride (the stored
+    // heads', also where the kernel's heads are pairs of them).
+    const int64_t head0 = (int64_t)b * S * sh.token_stride + (int64_t)kv * D;
     const uint16_t* kb = sh.k_new + head0;
     const uint16_t* vb = sh.v_new + head0;
 #pragma unroll
@@ -1257,7 +1259,7 @@ __device__ __forceinline__ void copy_new_tokens(const int32_t* __restrict__ seq_
       bad = true;
       continue;
     }
-    const int64_t src = (((int64_t)b * S + j) * sh.num_kv_heads + kv) * D + 8 * seg;
+    const int64_t src = ((int64_t)b * S + j) * sh.token_stride + (int64_t)kv * D + 8 * seg;
     const int64_t dst = (int64_t)pid * sh.page_stride + (int64_t)(pos % psize) * sh.token_stride +
                         kv * D + 8 * seg;
     const u32x4 x = *reinterpret_cast<const u32x4*>((is_v ? sh.v_new : sh.k_new) + src);
@@ -1593,14 +1595,18 @@ void mx_paged_decode_splitkv(
   if constexpr (kAppend) {
     // Fused append: the split holding the last schedule chunk also takes the new keys, as one
     // more chunk after its cache chunks in the waves' round-robin order.
+    // Paired waves: each head's two waves take the new keys of their own head.
     const bool last = c_hi * kChunk >= seq;
-    const NewTokens<kFp8> nt{sh, b, kv, ext.cache, last && wv == (c_end - c_lo) % NW,
+    const int hk = kPairW ? 2 * kv + (wv >> 1) : kv;       // the stored head this wave streams
+    const int wk = kPairW ? (wv & 1) : wv;                  // its place among the head's waves
+    constexpr int kHeadWaves = kPairW ? 2 : NW;
+    const NewTokens<kFp8> nt{sh, b, hk, ext.cache, last && wk == (c_end - c_lo) % kHeadWaves,
                        grp == 0,    ext.at,     bt_row, status};
-    stream_chunks<D, NBUF, NW, kCausal, KT, NewTokens<kFp8>, kFp8>(st, qop, kc, vc, bt_row, kv, c_lo, c_end, ext.cache,
-                                            c_mask, row_lim, wv, L::ktile(lds, wv), sh, bad_page,
-                                            nt);
+    stream_chunks<D, NBUF, kHeadWaves, kCausal, KT, NewTokens<kFp8>, kFp8>(
+        st, qop, kc, vc, bt_row, hk, c_lo, c_end, ext.cache, c_mask, row_lim, wk,
+        L::ktile(lds, wv), sh, bad_page, nt);
   } else if constexpr (kPairW) {
-    static_assert(NW == 4 && KT == 1 && !kAppend, "paired waves: four waves, one row tile");
+    static_assert(NW == 4 && KT == 1, "paired waves: four waves, one row tile");
     stream_chunks<D, NBUF, 2, kCausal, KT, NoExtraChunk, kFp8>(
         st, qop, kc, vc, bt_row, 2 * kv + (wv >> 1), c_lo, c_end, ext.cache, c_mask, row_lim,
         wv & 1, L::ktile(lds, wv), sh, bad_page);
@@ -1874,13 +1880,17 @@ void mx_paged_decode_balanced(
       if constexpr (kAppend) {
         // Fused append: the piece holding the unit's last schedule chunk also takes the new
         // keys, as one more chunk after its cache chunks in the waves' round-robin order.
-        const NewTokens<kFp8> nt{sh, b, kv, ext.cache, cb == n_b && wv == (c_end - ca) % NW,
+        // Paired waves: each head's two waves take the new keys of their own head.
+        const int hk = kPairW ? 2 * kv + (wv >> 1) : kv;   // the stored head this wave streams
+        const int wk = kPairW ? (wv & 1) : wv;              // its place among the head's waves
+        constexpr int kHeadWaves = kPairW ? 2 : NW;
+        const NewTokens<kFp8> nt{sh, b, hk, ext.cache, cb == n_b && wk == (c_end - ca) % kHeadWaves,
                            grp == 0, ext.at, bt_row, status};
-        stream_chunks<D, NBUF, NW, kCausal, KT, NewTokens<kFp8>, kFp8>(st, qop, kc, vc, bt_row, kv, ca, c_end,
-                                                ext.cache, c_mask, row_lim, wv,
-                                                L::ktile(lds, wv), sh, bad_page, nt);
+        stream_chunks<D, NBUF, kHeadWaves, kCausal, KT, NewTokens<kFp8>, kFp8>(
+            st, qop, kc, vc, bt_row, hk, ca, c_end, ext.cache, c_mask, row_lim, wk,
+            L::ktile(lds, wv), sh, bad_page, nt);
       } else if constexpr (kPairW) {
-        static_assert(NW == 4 && KT == 1 && !kAppend, "paired waves: four waves, one row tile");
+        static_assert(NW == 4 && KT == 1, "paired waves: four waves, one row tile");
         stream_chunks<D, NBUF, 2, kCausal, KT, NoExtraChunk, kFp8>(
             st, qop, kc, vc, bt_row, 2 * kv + (wv >> 1), ca, c_end, ext.cache, c_mask, row_lim,
             wv & 1, L::ktile(lds, wv), sh, bad_page);
@@ -2315,9 +2325,9 @@ int query_num_cus(int64_t* num_cus) {
 
 // Validates the shape and computes the split plan.  Performs no HIP call when num_cus > 0.
 // Whether an automatic plan runs adjacent KV heads in pairs, two waves per head
-// (MX_SCHEDULE_SPLIT_GRID_PAIRED, MX_SCHEDULE_BALANCED_PAIRED): bf16 decodes without a fused
-// append (pair_ok), head_dim 128, token rows of at least 2 KB (>= 8 KV heads, an even count) and
-// both heads' rows in one 16-row tile.
+// (MX_SCHEDULE_SPLIT_GRID_PAIRED, MX_SCHEDULE_BALANCED_PAIRED): bf16 caches (pair_ok), head_dim
+// 128, token rows of at least 2 KB (>= 8 KV heads, an even count) and both heads' rows in one
+// 16-row tile.
 bool pair_heads(bool pair_ok, int64_t num_splits, int64_t head_dim, int64_t num_kv_heads,
                 int64_t rows) {
   return pair_ok && num_splits == 0 && head_dim == 128 && num_kv_heads % 2 == 0 &&
@@ -2670,10 +2680,13 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
                          reinterpret_cast<uint32_t*>(ws + plan.counter_offset), status, sh);
     };
     if (paired) {
-      // make_plan pairs only bf16 decodes without a fused append, at head_dim 128, one tile.
+      // make_plan pairs only bf16 decodes at head_dim 128 with one tile.
       if constexpr (D == 128 && KT == 1) {
-        if (kv.fp8 || append) return hipErrorInvalidValue;
-        go(mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, false, false, true>, k16, v16);
+        if (kv.fp8) return hipErrorInvalidValue;
+        if (append)
+          go(mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, true, false, true>, k16, v16);
+        else
+          go(mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, false, false, true>, k16, v16);
       } else {
         return hipErrorInvalidValue;
       }
@@ -2705,10 +2718,13 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
                          reinterpret_cast<uint32_t*>(ws + kStatusBytes), status, sh);
     };
     if (paired) {
-      // make_plan pairs only bf16 decodes without a fused append, at head_dim 128, one tile.
+      // make_plan pairs only bf16 decodes at head_dim 128 with one tile.
       if constexpr (D == 128 && KT == 1) {
-        if (kv.fp8 || append) return hipErrorInvalidValue;
-        go(mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT, false, false, true>, k16, v16);
+        if (kv.fp8) return hipErrorInvalidValue;
+        if (append)
+          go(mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT, true, false, true>, k16, v16);
+        else
+          go(mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT, false, false, true>, k16, v16);
       } else {
         return hipErrorInvalidValue;
       }
@@ -3250,7 +3266,7 @@ static int decode_append_impl(const void* q, const void* k_new, const void* v_ne
   const KernelHeads kh = kernel_heads(seqlen_q, num_heads, num_kv_heads, head_dim, kv.fp8);
   st = prepare_decode(q, k_cache, v_cache, out, batch, seqlen_q, num_heads, kh.kv_heads,
                       kh.head_dim, page_size, num_pages, max_pages_per_seq, max_seq_len, causal,
-                      scale, num_splits, &workspace, workspace_bytes, 0, stream, false, &plan);
+                      scale, num_splits, &workspace, workspace_bytes, 0, stream, !kv.fp8, &plan);
   if (st != MX_STATUS_OK) return st;
   AppendArgs app;
   if (seqlen_new >= 1 && seqlen_new <= kChunk) {

@@ -159,6 +159,34 @@ def test_append_and_attend_matches_the_oracle(S, sq, causal, ns):
     assert read_device_status() == 0
 
 
+@pytest.mark.parametrize("lens,schedule", [
+    ([0, 1, 15, 16, 100, 1000, 2047, 4000] * 8, "balanced_paired"),
+    ([0, 1, 17, 1025, 9000, 16000], "split_grid_paired"),
+])
+@pytest.mark.parametrize("S,sq,causal", [(1, 1, False), (5, 2, True), (17, 2, True)])
+def test_append_and_attend_on_paired_heads(lens, schedule, S, sq, causal):
+    """The automatic plan pairs the KV heads of these shapes (two waves per head): the wave
+    streaming a head takes that head's new keys and writes them to the cache.  Pools bit-exact
+    against the oracle's append, output within tolerance; S = 17 runs the append kernel and
+    then the paired decode."""
+    from mx_flash_attn_kernel_opt__amd import paged_gqa_decode_append, plan
+    from oracle import paged_decode_append_reference
+    k, v, table, kn, vn, q, lens_t = _fused_case(lens, S, sq, seed=S + 31 * sq)
+    assert plan(len(lens), 32, 8, 128, 16, table.shape[1], seqlen_q=sq)["schedule"] == schedule
+    ref, k2, v2, flags = paged_decode_append_reference(q, kn, vn, k, v, table, lens_t,
+                                                       causal=causal)
+    assert not flags
+    kd, vd = k.to(DEV), v.to(DEV)
+    label = f"paired append+attend {schedule} S={S} sq={sq} causal={causal}"
+    print(label, flush=True)
+    out = paged_gqa_decode_append(q.to(DEV), kn.to(DEV), vn.to(DEV), kd, vd, table.to(DEV),
+                                  lens_t.to(DEV), causal=causal)
+    torch.cuda.synchronize()
+    assert torch.equal(kd.cpu(), k2) and torch.equal(vd.cpu(), v2), label
+    assert_close_to_oracle(out, ref, label)
+    assert read_device_status() == 0
+
+
 @pytest.mark.parametrize("ns", [0, 3, -5])
 @pytest.mark.parametrize("D,P,Hkv,G,S,sq", [
     (64, 16, 2, 4, 6, 3),       # head_dim 64 (two waves per workgroup)
