@@ -614,16 +614,18 @@ def _paired_inputs(sq=1, seed=0, lens=PAIR_LENS, Hq=32, Hkv=8, P=16):
     return W.make_inputs(spec, seed=seed, device=DEV)
 
 
-@pytest.mark.parametrize("Hq,Hkv,P", [(32, 8, 16), (32, 8, 64), (64, 8, 16)])
-def test_paired_split_grid_matches_oracle(Hq, Hkv, P):
-    """The automatic plan pairs heads on these shapes; every sequence (empty, one token, a
-    page boundary plus one, a chunk past a split, long) against the oracle; repeated calls are
-    identical (the merge counters reset themselves) and the device status stays clean."""
+@pytest.mark.parametrize("Hq,Hkv,P", [(32, 8, 16), (32, 8, 64), (64, 8, 16), (64, 16, 32)])
+def test_paired_heads_match_oracle(Hq, Hkv, P):
+    """The automatic plan pairs heads on these shapes (the split grid with 8 KV heads; with 16
+    the 96 units take the balanced schedule); every sequence (empty, one token, a page boundary
+    plus one, a chunk past a split, long) against the oracle; repeated calls are identical (the
+    merge counters reset themselves) and the device status stays clean."""
     from mx_flash_attn_kernel_opt__amd import plan
     inp = _paired_inputs(Hq=Hq, Hkv=Hkv, P=P, seed=Hq + P)
     s = inp.spec
     p = plan(s.batch, Hq, Hkv, 128, P, s.max_pages)
-    assert p["schedule"] == "split_grid_paired" and p["launches"] == 1
+    expect = "split_grid_paired" if Hkv == 8 else "balanced_paired"
+    assert p["schedule"] == expect and p["launches"] == 1
     out = _decode(inp).clone()
     _check(inp, out, label=f"paired Hq={Hq} Hkv={Hkv} P={P}")
     assert not out[0].float().abs().any().item()          # the empty sequence
