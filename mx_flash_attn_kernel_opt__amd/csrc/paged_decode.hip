@@ -1279,30 +1279,40 @@ constexpr int kMergeFanIn = 8;
 constexpr int kMaxMergeItems = 8 * 8 * 8 * 8;
 
 // Cross-workgroup handoff of partials (the split grid's in-kernel merge and the balanced
-// kernel's merge tree).  Partials are stored and loaded with relaxed agent-scope atomic
-// accesses, which keep each location coherent across the device's XCDs with no L2 write-back
-// (gfx950: global_store / global_load with sc1).  The order between the stores of the pieces
-// and the loads of the workgroup that merges them comes from the arrival counter (arrive_last).
-// A plain-store variant with __threadfence() in every thread was measured first: it writes back
-// the L2 per wave, and config 2 with 1 024 workgroups ran 505 us instead of 174.
-__device__ __forceinline__ void store_partial4(float* p, f32x4 v) {
-  const u32x4 u = __builtin_bit_cast(u32x4, v);
-  const uint64_t lo = (uint64_t)u[0] | ((uint64_t)u[1] << 32);
-  const uint64_t hi = (uint64_t)u[2] | ((uint64_t)u[3] << 32);
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(p) + 1, hi, __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
+// kernel's merge tree).  Partials are stored and loaded with agent-coherent accesses, which keep
+// each location coherent across the device's XCDs with no L2 write-back: the sc1 cache policy
+// that relaxed agent-scope atomic accesses carry on gfx950 (global_store / global_load ... sc1).
+// The 16-byte row pieces go through buffer instructions with that policy (buffer_store_dwordx4
+// / buffer_load_dwordx4 ... sc1) over a resource based at the partial region, whose byte
+// offsets are 32-bit: the host keeps every region read this way below 2^31 bytes
+// (kMaxHandoffBytes).  Two 8-byte atomic accesses per piece instead wrote each 64-byte line
+// through twice (WRITE_SIZE twice the partial bytes); interleaved A/B against them, outputs
+// bitwise equal: long B=1 128K 85.0 against 85.8 us, contest cases 10 and 14 (B=1, 64 splits)
+// 11.35 against 11.75 and 27.0 against 27.6 us, the balanced shapes within +-0.3 us.  The
+// order between the stores of the pieces and the loads of the workgroup that merges them comes
+// from the arrival counter (arrive_last).  A plain-store variant with __threadfence() in every
+// thread was measured first: it writes back the L2 per wave, and config 2 with 1 024 workgroups
+// ran 505 us instead of 174.
+constexpr int kCachePolicySc1 = 16;  // buffer intrinsics' aux bit for sc1
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(const float* base) {
+  // Raw buffer over [base, base + 2^31 - 1): stride 0, dword 3 = 0x00020000 (32-bit data, no
+  // swizzle), as for every gfx9 raw buffer.
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, 0x7fffffff,
+                                           0x00020000);
+}
+__device__ __forceinline__ void store_partial4(const float* base, float* p, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), partial_rsrc(base),
+                                         (int)((const char*)p - (const char*)base), 0,
+                                         kCachePolicySc1);
 }
 __device__ __forceinline__ void store_partial1(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ f32x4 load_partial4(const float* p) {
-  const uint64_t lo = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
-  const uint64_t hi = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p) + 1,
-                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const u32x4 u = {(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
-  return __builtin_bit_cast(f32x4, u);
+__device__ __forceinline__ f32x4 load_partial4(const float* base, const float* p) {
+  return __builtin_bit_cast(
+      f32x4, __builtin_amdgcn_raw_buffer_load_b128(partial_rsrc(base),
+                                                   (int)((const char*)p - (const char*)base), 0,
+                                                   kCachePolicySc1));
 }
 __device__ __forceinline__ float load_partial1(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1369,7 +1379,7 @@ __device__ __forceinline__ void merge_elems(const Tree& tree, int e0, int total,
     for (int t = 0; t < W; ++t) {
       const int sl = gslot + (t < gsize ? t : 0) * stride;
       ls[q][t] = load_partial1(tree.lse(hh[q], sl));
-      vs[q][t] = load_partial4(tree.o(hh[q], sl) + d[q]);
+      vs[q][t] = load_partial4(tree.part_o, tree.o(hh[q], sl) + d[q]);
     }
   }
 #pragma unroll
@@ -1396,7 +1406,7 @@ __device__ __forceinline__ void merge_elems(const Tree& tree, int e0, int total,
     if (final) {
       tree.store(hh[q], d[q], acc, lse);
     } else {
-      store_partial4(tree.o(hh[q], gslot) + d[q], acc);
+      store_partial4(tree.part_o, tree.o(hh[q], gslot) + d[q], acc);
       if (d[q] == 0) s_lse[hh[q]] = lse;
     }
   }
@@ -1632,7 +1642,7 @@ void mx_paged_decode_splitkv(
     if (single) {
       store_row4<D>(out, sh, row, d, o, lse);
     } else if (sh.fused_combine) {  // read back by another workgroup of this launch
-      store_partial4(part_o + (row * sh.num_splits + split) * D + d, o);
+      store_partial4(part_o, part_o + (row * sh.num_splits + split) * D + d, o);
       if (d == 0) store_partial1(part_lse + row * sh.num_splits + split, lse);
     } else {                        // read by the combine kernel of the next launch
       *reinterpret_cast<f32x4*>(part_o + (row * sh.num_splits + split) * D + d) = o;
@@ -1931,7 +1941,7 @@ void mx_paged_decode_balanced(
               o = merged_head_pair<D>(lds, hh, d, lse, sh);
             else
               o = merged_head<D, NW, KT>(lds, hh, d, lse);
-            store_partial4(po + hh * D + d, o);
+            store_partial4(part_o, po + hh * D + d, o);
             if (d == 0) store_partial1(pl + hh, lse);
           }
         }
@@ -2243,10 +2253,16 @@ constexpr int64_t kMaxMergeRows = int64_t(1) << 25;  // mx_lse_merge: 64 * rows 
 int64_t groups_per_cu(int64_t head_dim) { return head_dim == 64 ? 2 : 1; }
 
 // Whether the split grid's units merge their splits in-kernel (one launch): each level of the
-// counter region must hold ceil(splits / kMergeFanIn) counters per unit, and the tree's levels
-// cover at most kMaxMergeItems splits.  Otherwise the combine kernel merges in a second launch.
-bool split_tree_fits(int64_t units, int64_t splits) {
-  return splits <= kMaxMergeItems && units * ceil_div(splits, kMergeFanIn) <= kMaxSlots;
+// counter region must hold ceil(splits / kMergeFanIn) counters per unit, the tree's levels
+// cover at most kMaxMergeItems splits, and the o partials (o_bytes) stay within the 32-bit
+// offsets of the handoff's buffer accesses.  Otherwise the combine kernel merges in a second
+// launch.
+constexpr int64_t kMaxHandoffBytes = 0x7fffffff;
+// The balanced kernel's partial slots always fit: slots <= kMaxSlots of at most 64 rows.
+static_assert((int64_t)kMaxSlots * 64 * 256 * 4 <= kMaxHandoffBytes, "balanced partials");
+bool split_tree_fits(int64_t units, int64_t splits, int64_t o_bytes) {
+  return splits <= kMaxMergeItems && units * ceil_div(splits, kMergeFanIn) <= kMaxSlots &&
+         o_bytes <= kMaxHandoffBytes;
 }
 
 // Balanced schedule: chunk positions charged per unit on top of its chunks, for its query load,
@@ -2706,7 +2722,8 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   // One launch (the splits of each unit merge through an in-kernel tree) when the units' arrival
   // counters fit the counter region and the caller did not ask for the two phases separately.
   const bool fused = phase == 0 && plan.splits > 1 &&
-                     split_tree_fits(batch * kernel_kv * plan.row_tiles, plan.splits);
+                     split_tree_fits(batch * kernel_kv * plan.row_tiles, plan.splits,
+                                     plan.workspace_bytes - plan.o_offset);
   sh.split_groups = (int)ceil_div(plan.splits, kMergeFanIn);
   sh.fused_combine = fused ? 1 : 0;
   if (phase != MX_PHASE_COMBINE_ONLY) {

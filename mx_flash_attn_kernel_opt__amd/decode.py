@@ -20,6 +20,7 @@ from . import _lib
 MERGE_FAN_IN = 8             # kMergeFanIn in csrc/paged_decode.hip
 MAX_MERGE_ITEMS = 8 ** 4     # kMaxMergeItems
 COUNTER_SLOTS = 4096 + 8192  # kMaxSlots in csrc/paged_decode.hip
+MAX_HANDOFF_BYTES = 2**31 - 1  # kMaxHandoffBytes
 
 
 def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
@@ -60,13 +61,16 @@ def plan(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, page_size
                 _lib.MX_SCHEDULE_BALANCED_PAIRED: "balanced_paired"}[sch.value]
     # Launches of a phase-0 call: the balanced schedule and the split grid with one split are
     # one launch; the split grid merges its splits through an in-kernel tree when there are at
-    # most MAX_MERGE_ITEMS and every unit's ceil(splits / MERGE_FAN_IN) arrival counters fit the
-    # counter region, else a combine kernel follows (csrc/paged_decode.hip, split_tree_fits).
-    # The split grid launches units x splits workgroups.
+    # most MAX_MERGE_ITEMS, every unit's ceil(splits / MERGE_FAN_IN) arrival counters fit the
+    # counter region and the fp32 o partials (one row per query row and split) take at most
+    # MAX_HANDOFF_BYTES, else a combine kernel follows (csrc/paged_decode.hip,
+    # split_tree_fits).  The split grid launches units x splits workgroups.
     units = wgs.value // max(ns.value, 1)
+    o_bytes = batch * seqlen_q * num_heads * ns.value * head_dim * 4
     two = (schedule.startswith("split_grid") and ns.value > 1 and
            (ns.value > MAX_MERGE_ITEMS or
-            units * math.ceil(ns.value / MERGE_FAN_IN) > COUNTER_SLOTS))
+            units * math.ceil(ns.value / MERGE_FAN_IN) > COUNTER_SLOTS or
+            o_bytes > MAX_HANDOFF_BYTES))
     return {"schedule": schedule, "splits": ns.value, "tokens_per_split": tps.value,
             "workgroups": wgs.value, "workspace_bytes": ws.value, "launches": 2 if two else 1}
 
