@@ -2341,9 +2341,9 @@ int query_num_cus(int64_t* num_cus) {
 
 // Validates the shape and computes the split plan.  Performs no HIP call when num_cus > 0.
 // Whether an automatic plan runs adjacent KV heads in pairs, two waves per head
-// (MX_SCHEDULE_SPLIT_GRID_PAIRED, MX_SCHEDULE_BALANCED_PAIRED): bf16 caches (pair_ok), head_dim
-// 128, token rows of at least 2 KB (>= 8 KV heads, an even count) and both heads' rows in one
-// 16-row tile.
+// (MX_SCHEDULE_SPLIT_GRID_PAIRED, MX_SCHEDULE_BALANCED_PAIRED): calls that allow it (pair_ok:
+// pair_ok_for), head_dim 128, at least 8 KV heads, an even count (token rows of at least 2 KB
+// in bf16, 1 KB in fp8), and both heads' rows in one 16-row tile.
 bool pair_heads(bool pair_ok, int64_t num_splits, int64_t head_dim, int64_t num_kv_heads,
                 int64_t rows) {
   return pair_ok && num_splits == 0 && head_dim == 128 && num_kv_heads % 2 == 0 &&
@@ -2615,6 +2615,15 @@ KernelHeads kernel_heads(int64_t seqlen_q, int64_t num_heads, int64_t num_kv_hea
   return {num_kv_heads / 2, 128, (int)(num_heads / num_kv_heads)};
 }
 
+// Whether a decode may run KV heads in pairs (pair_heads): bf16 caches, and fp8 caches whose
+// kernel heads are the stored heads (not the head_dim-64 pairs of kernel_heads) when no append
+// is fused in.  Paired fp8, interleaved A/B against single heads on cold pools: config 2's
+// shape 89.5 and 94.7 against 94.0 and 96.8 us, the B=32 16K sweep 182.4 against 199.7 us,
+// long B=1 128K 54.1 against 55.0, long B=4 32K 53.6 against 53.2.
+bool pair_ok_for(bool fp8, const KernelHeads& kh, bool append) {
+  return !fp8 || (kh.pair_group == 0 && !append);
+}
+
 // Register ring depth of the fp8 kernels (an fp8 chunk takes half the registers of a bf16 one).
 // (A/B on 512 MB fp8 caches, chunks per ring 2/3/4/6: D=64 173.6/174.7/183.0/186.2 us, D=128
 // config-2 shape 95.8/93.2/95.7/96.4 us, D=256 1/2/3/6 chunks 94.5/93.3-96.7/94.9/104.1 us.)
@@ -2696,10 +2705,12 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
                          reinterpret_cast<uint32_t*>(ws + plan.counter_offset), status, sh);
     };
     if (paired) {
-      // make_plan pairs only bf16 decodes at head_dim 128 with one tile.
+      // make_plan pairs only head_dim 128 with one tile, and fp8 caches without an append.
       if constexpr (D == 128 && KT == 1) {
-        if (kv.fp8) return hipErrorInvalidValue;
-        if (append)
+        if (kv.fp8 && append) return hipErrorInvalidValue;
+        if (kv.fp8)
+          go(mx_paged_decode_balanced<D, kNBUF8, kNW, kCausal, KT, false, true, true>, k8, v8);
+        else if (append)
           go(mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, true, false, true>, k16, v16);
         else
           go(mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, false, false, true>, k16, v16);
@@ -2735,10 +2746,12 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
                          reinterpret_cast<uint32_t*>(ws + kStatusBytes), status, sh);
     };
     if (paired) {
-      // make_plan pairs only bf16 decodes at head_dim 128 with one tile.
+      // make_plan pairs only head_dim 128 with one tile, and fp8 caches without an append.
       if constexpr (D == 128 && KT == 1) {
-        if (kv.fp8) return hipErrorInvalidValue;
-        if (append)
+        if (kv.fp8 && append) return hipErrorInvalidValue;
+        if (kv.fp8)
+          go(mx_paged_decode_splitkv<D, kNBUF8, kNW, kCausal, KT, false, true, true>, k8, v8);
+        else if (append)
           go(mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT, true, false, true>, k16, v16);
         else
           go(mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT, false, false, true>, k16, v16);
@@ -2786,7 +2799,8 @@ static int report_plan(bool fp8, int64_t batch, int64_t seqlen_q, int64_t num_he
   Plan plan;
   const KernelHeads kh = kernel_heads(seqlen_q, num_heads, num_kv_heads, head_dim, fp8);
   const int st = make_plan(batch, seqlen_q, num_heads, kh.kv_heads, kh.head_dim, page_size,
-                           max_pages_per_seq, max_seq_len, num_splits, num_cus, !fp8, &plan);
+                           max_pages_per_seq, max_seq_len, num_splits, num_cus,
+                           pair_ok_for(fp8, kh, false), &plan);
   if (st != MX_STATUS_OK) return st;
   if (schedule_out) *schedule_out = plan.schedule;
   if (splits_out) *splits_out = plan.splits;
@@ -2826,15 +2840,19 @@ int64_t mx_paged_gqa_decode_workspace_size(int64_t batch, int64_t seqlen_q, int6
                                            int64_t num_kv_heads, int64_t head_dim,
                                            int64_t page_size, int64_t max_pages_per_seq,
                                            int64_t max_seq_len, int64_t num_splits) {
-  // The size covers the call on a bf16 and on an fp8 cache (whose kernel heads may differ).
+  // The size covers the call on a bf16 and on an fp8 cache (whose kernel heads may differ),
+  // with and without a fused append (an fp8 decode may pair KV heads where its append does not).
   int64_t bytes = 0;
   for (const bool fp8 : {false, true}) {
-    Plan plan;
-    const KernelHeads kh = kernel_heads(seqlen_q, num_heads, num_kv_heads, head_dim, fp8);
-    const int st = make_plan(batch, seqlen_q, num_heads, kh.kv_heads, kh.head_dim, page_size,
-                             max_pages_per_seq, max_seq_len, num_splits, 0, !fp8, &plan);
-    if (st != MX_STATUS_OK) return st;
-    bytes = std::max(bytes, plan.workspace_bytes);
+    for (const bool append : {false, true}) {
+      Plan plan;
+      const KernelHeads kh = kernel_heads(seqlen_q, num_heads, num_kv_heads, head_dim, fp8);
+      const int st = make_plan(batch, seqlen_q, num_heads, kh.kv_heads, kh.head_dim, page_size,
+                               max_pages_per_seq, max_seq_len, num_splits, 0,
+                               pair_ok_for(fp8, kh, append), &plan);
+      if (st != MX_STATUS_OK) return st;
+      bytes = std::max(bytes, plan.workspace_bytes);
+    }
   }
   ok();
   return bytes;
@@ -2927,7 +2945,8 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* o
   const int st = prepare_decode(q, k_cache, v_cache, out, batch, seqlen_q, num_heads,
                                 kh.kv_heads, kh.head_dim, page_size, num_pages, max_pages_per_seq,
                                 max_seq_len, causal, scale, num_splits, &workspace,
-                                workspace_bytes, phase, stream, !kv.fp8, &plan);
+                                workspace_bytes, phase, stream, pair_ok_for(kv.fp8, kh, false),
+                                &plan);
   if (st != MX_STATUS_OK) return st;
   return run_decode(plan, q, k_cache, v_cache, out, o_out, lse_out, seq_lens, block_table, batch,
                     seqlen_q, num_heads, kh.kv_heads, kh.head_dim, page_size, num_pages,
@@ -3283,7 +3302,8 @@ static int decode_append_impl(const void* q, const void* k_new, const void* v_ne
   const KernelHeads kh = kernel_heads(seqlen_q, num_heads, num_kv_heads, head_dim, kv.fp8);
   st = prepare_decode(q, k_cache, v_cache, out, batch, seqlen_q, num_heads, kh.kv_heads,
                       kh.head_dim, page_size, num_pages, max_pages_per_seq, max_seq_len, causal,
-                      scale, num_splits, &workspace, workspace_bytes, 0, stream, !kv.fp8, &plan);
+                      scale, num_splits, &workspace, workspace_bytes, 0, stream,
+                      pair_ok_for(kv.fp8, kh, true), &plan);
   if (st != MX_STATUS_OK) return st;
   AppendArgs app;
   if (seqlen_new >= 1 && seqlen_new <= kChunk) {

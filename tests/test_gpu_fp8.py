@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from conftest import assert_close_to_oracle
-from mx_flash_attn_kernel_opt__amd import paged_gqa_decode, read_device_status
+from mx_flash_attn_kernel_opt__amd import paged_gqa_decode, plan, read_device_status
 from oracle import paged_decode_fp8_reference
 
 pytestmark = pytest.mark.gpu
@@ -55,6 +55,27 @@ def test_fp8_decode_matches_the_oracle(D, Hq, Hkv, P, ns):
     print(label, flush=True)
     out = _run(q, k8, v8, table, lt, ns=ns, k_scale=0.7, v_scale=1.3)
     ref = paged_decode_fp8_reference(q, k8, v8, table, lt, k_scale=0.7, v_scale=1.3)
+    assert_close_to_oracle(out, ref, label)
+    assert read_device_status() == 0
+
+
+@pytest.mark.parametrize("B,Hq,L,sched,causal", [
+    (16, 32, 4096, "balanced_paired", False),     # config 2's heads: 1 KB fp8 token rows
+    (16, 32, 4096, "balanced_paired", True),      # one token: causal is the same keys
+    (2, 64, 65536, "split_grid_paired", False),   # long context, 32 paired splits of 2 048
+])
+def test_fp8_paired_heads_match_the_oracle(B, Hq, L, sched, causal):
+    """fp8 caches with 8 KV heads at head_dim 128 run adjacent heads in pairs, two waves per
+    head, on both schedules; ragged lengths up to the capacity L."""
+    Hkv, D, P = 8, 128, 16
+    assert plan(B, Hq, Hkv, D, P, L // P, L, 0, num_cus=256, fp8=True)["schedule"] == sched
+    r = random.Random(B + L)
+    lens = [L] + [r.randint(1, L) for _ in range(B - 2)] + [r.randint(1, 40)]
+    q, k8, v8, table, lt = _case(lens, Hq, Hkv, D, P, seed=L + int(causal))
+    label = f"fp8 paired B={B} Hq={Hq} L={L} {sched} causal={causal}"
+    print(label, flush=True)
+    out = _run(q, k8, v8, table, lt, causal=causal, k_scale=0.8, v_scale=1.2)
+    ref = paged_decode_fp8_reference(q, k8, v8, table, lt, k_scale=0.8, v_scale=1.2)
     assert_close_to_oracle(out, ref, label)
     assert read_device_status() == 0
 

@@ -235,7 +235,7 @@ def test_policy_on_the_north_star_configs():
     (1, 64, 8, 128, 131072, 1, False, 0, "split_grid_paired", 64),
     (4, 64, 8, 128, 32768, 1, False, 0, "split_grid_paired", 16),
     (1, 64, 8, 128, 32768, 1, False, 0, "split_grid", 32),    # paired splits of 512 tokens
-    (1, 64, 8, 128, 131072, 1, True, 0, "split_grid", 32),    # fp8 caches are not paired
+    (1, 64, 8, 128, 131072, 1, True, 0, "split_grid_paired", 64),  # fp8: 1 KB token rows
     (1, 64, 8, 128, 131072, 1, False, 32, "split_grid", 32),  # explicit split counts are not
     (1, 56, 7, 128, 131072, 1, False, 0, "split_grid", 37),   # odd KV head count
     (1, 64, 4, 128, 131072, 1, False, 0, "split_grid", 64),   # group 16: 32 rows per pair
