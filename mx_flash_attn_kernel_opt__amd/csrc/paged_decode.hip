@@ -2616,12 +2616,12 @@ KernelHeads kernel_heads(int64_t seqlen_q, int64_t num_heads, int64_t num_kv_hea
 }
 
 // Whether a decode may run KV heads in pairs (pair_heads): bf16 caches, and fp8 caches whose
-// kernel heads are the stored heads (not the head_dim-64 pairs of kernel_heads) when no append
-// is fused in.  Paired fp8, interleaved A/B against single heads on cold pools: config 2's
-// shape 89.5 and 94.7 against 94.0 and 96.8 us, the B=32 16K sweep 182.4 against 199.7 us,
-// long B=1 128K 54.1 against 55.0, long B=4 32K 53.6 against 53.2.
-bool pair_ok_for(bool fp8, const KernelHeads& kh, bool append) {
-  return !fp8 || (kh.pair_group == 0 && !append);
+// kernel heads are the stored heads (not the head_dim-64 pairs of kernel_heads), with or
+// without a fused append.  Paired fp8, interleaved A/B against single heads on cold pools:
+// config 2's shape 89.5 and 94.7 against 94.0 and 96.8 us, the B=32 16K sweep 182.4 against
+// 199.7 us, long B=1 128K 54.1 against 55.0, long B=4 32K 53.6 against 53.2.
+bool pair_ok_for(bool fp8, const KernelHeads& kh) {
+  return !fp8 || kh.pair_group == 0;
 }
 
 // Register ring depth of the fp8 kernels (an fp8 chunk takes half the registers of a bf16 one).
@@ -2705,10 +2705,11 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
                          reinterpret_cast<uint32_t*>(ws + plan.counter_offset), status, sh);
     };
     if (paired) {
-      // make_plan pairs only head_dim 128 with one tile, and fp8 caches without an append.
+      // make_plan pairs only head_dim 128 with one tile.
       if constexpr (D == 128 && KT == 1) {
-        if (kv.fp8 && append) return hipErrorInvalidValue;
-        if (kv.fp8)
+        if (kv.fp8 && append)
+          go(mx_paged_decode_balanced<D, kNBUF8, kNW, kCausal, KT, true, true, true>, k8, v8);
+        else if (kv.fp8)
           go(mx_paged_decode_balanced<D, kNBUF8, kNW, kCausal, KT, false, true, true>, k8, v8);
         else if (append)
           go(mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, true, false, true>, k16, v16);
@@ -2746,10 +2747,11 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
                          reinterpret_cast<uint32_t*>(ws + kStatusBytes), status, sh);
     };
     if (paired) {
-      // make_plan pairs only head_dim 128 with one tile, and fp8 caches without an append.
+      // make_plan pairs only head_dim 128 with one tile.
       if constexpr (D == 128 && KT == 1) {
-        if (kv.fp8 && append) return hipErrorInvalidValue;
-        if (kv.fp8)
+        if (kv.fp8 && append)
+          go(mx_paged_decode_splitkv<D, kNBUF8, kNW, kCausal, KT, true, true, true>, k8, v8);
+        else if (kv.fp8)
           go(mx_paged_decode_splitkv<D, kNBUF8, kNW, kCausal, KT, false, true, true>, k8, v8);
         else if (append)
           go(mx_paged_decode_splitkv<D, kNBUF, kNW, kCausal, KT, true, false, true>, k16, v16);
@@ -2800,7 +2802,7 @@ static int report_plan(bool fp8, int64_t batch, int64_t seqlen_q, int64_t num_he
   const KernelHeads kh = kernel_heads(seqlen_q, num_heads, num_kv_heads, head_dim, fp8);
   const int st = make_plan(batch, seqlen_q, num_heads, kh.kv_heads, kh.head_dim, page_size,
                            max_pages_per_seq, max_seq_len, num_splits, num_cus,
-                           pair_ok_for(fp8, kh, false), &plan);
+                           pair_ok_for(fp8, kh), &plan);
   if (st != MX_STATUS_OK) return st;
   if (schedule_out) *schedule_out = plan.schedule;
   if (splits_out) *splits_out = plan.splits;
@@ -2840,19 +2842,16 @@ int64_t mx_paged_gqa_decode_workspace_size(int64_t batch, int64_t seqlen_q, int6
                                            int64_t num_kv_heads, int64_t head_dim,
                                            int64_t page_size, int64_t max_pages_per_seq,
                                            int64_t max_seq_len, int64_t num_splits) {
-  // The size covers the call on a bf16 and on an fp8 cache (whose kernel heads may differ),
-  // with and without a fused append (an fp8 decode may pair KV heads where its append does not).
+  // The size covers the call on a bf16 and on an fp8 cache (whose kernel heads may differ).
   int64_t bytes = 0;
   for (const bool fp8 : {false, true}) {
-    for (const bool append : {false, true}) {
-      Plan plan;
-      const KernelHeads kh = kernel_heads(seqlen_q, num_heads, num_kv_heads, head_dim, fp8);
-      const int st = make_plan(batch, seqlen_q, num_heads, kh.kv_heads, kh.head_dim, page_size,
-                               max_pages_per_seq, max_seq_len, num_splits, 0,
-                               pair_ok_for(fp8, kh, append), &plan);
-      if (st != MX_STATUS_OK) return st;
-      bytes = std::max(bytes, plan.workspace_bytes);
-    }
+    Plan plan;
+    const KernelHeads kh = kernel_heads(seqlen_q, num_heads, num_kv_heads, head_dim, fp8);
+    const int st = make_plan(batch, seqlen_q, num_heads, kh.kv_heads, kh.head_dim, page_size,
+                             max_pages_per_seq, max_seq_len, num_splits, 0, pair_ok_for(fp8, kh),
+                             &plan);
+    if (st != MX_STATUS_OK) return st;
+    bytes = std::max(bytes, plan.workspace_bytes);
   }
   ok();
   return bytes;
@@ -2945,7 +2944,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* o
   const int st = prepare_decode(q, k_cache, v_cache, out, batch, seqlen_q, num_heads,
                                 kh.kv_heads, kh.head_dim, page_size, num_pages, max_pages_per_seq,
                                 max_seq_len, causal, scale, num_splits, &workspace,
-                                workspace_bytes, phase, stream, pair_ok_for(kv.fp8, kh, false),
+                                workspace_bytes, phase, stream, pair_ok_for(kv.fp8, kh),
                                 &plan);
   if (st != MX_STATUS_OK) return st;
   return run_decode(plan, q, k_cache, v_cache, out, o_out, lse_out, seq_lens, block_table, batch,
@@ -3303,7 +3302,7 @@ static int decode_append_impl(const void* q, const void* k_new, const void* v_ne
   st = prepare_decode(q, k_cache, v_cache, out, batch, seqlen_q, num_heads, kh.kv_heads,
                       kh.head_dim, page_size, num_pages, max_pages_per_seq, max_seq_len, causal,
                       scale, num_splits, &workspace, workspace_bytes, 0, stream,
-                      pair_ok_for(kv.fp8, kh, true), &plan);
+                      pair_ok_for(kv.fp8, kh), &plan);
   if (st != MX_STATUS_OK) return st;
   AppendArgs app;
   if (seqlen_new >= 1 && seqlen_new <= kChunk) {

@@ -308,6 +308,44 @@ def test_fp8_decode_append_matches_the_oracle(S, SQ, causal, ns, D, Hq, Hkv):
     assert read_device_status() == 0
 
 
+@pytest.mark.parametrize("B,width,S,SQ,causal,sched", [
+    (16, 256, 1, 1, False, "balanced_paired"),
+    (16, 256, 3, 2, True, "balanced_paired"),    # 2 query tokens x group 4 per head
+    (2, 4096, 1, 1, False, "split_grid_paired"),
+])
+def test_fp8_decode_append_on_paired_heads(B, width, S, SQ, causal, sched):
+    """Append-and-attend on an fp8 cache with 8 KV heads at head_dim 128, where both schedules
+    run adjacent heads in pairs: each head's waves quantize and write their own head's new rows
+    (the caches bit-exact against the append oracle) and attend them (the output within the
+    tolerance)."""
+    from mx_flash_attn_kernel_opt__amd import paged_gqa_decode_append
+    from oracle import paged_kv_append_reference
+    Hq, Hkv, D, P = 32, 8, 128, 16
+    cap = width * P
+    assert plan(B, Hq, Hkv, D, P, width, cap, 0, num_cus=256, seqlen_q=SQ,
+                fp8=True)["schedule"] == sched
+    kn, vn, k8, v8, table, lens = _append_case(B, S, Hkv, D, P, width, seed=B * S + width,
+                                               specials=False)
+    g = torch.Generator().manual_seed(B + S)
+    shape = (B, Hq, D) if SQ == 1 else (B, SQ, Hq, D)
+    q = (torch.randn(*shape, generator=g) * 0.5).to(torch.bfloat16)
+    kn, vn = kn.float().clamp(-40, 40).to(torch.bfloat16), (vn.float() * 0.25).to(torch.bfloat16)
+    ks, vs = 0.4, 0.8
+    label = f"fp8 paired decode+append B={B} cap={cap} S={S} SQ={SQ} causal={causal}"
+    print(label, flush=True)
+    kd, vd = k8.to(DEV), v8.to(DEV)
+    out = paged_gqa_decode_append(q.to(DEV), kn.to(DEV), vn.to(DEV), kd, vd, table.to(DEV),
+                                  lens.to(DEV), causal=causal, k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    kr, vr, _ = paged_kv_append_reference(kn, vn, k8, v8, table, lens, k_scale=ks, v_scale=vs)
+    assert torch.equal(kd.cpu().view(torch.uint8), kr.view(torch.uint8)), label
+    assert torch.equal(vd.cpu().view(torch.uint8), vr.view(torch.uint8)), label
+    ref = paged_decode_fp8_reference(q, kr, vr, table, lens + S, k_scale=ks, v_scale=vs,
+                                     causal=causal)
+    assert_close_to_oracle(out.cpu(), ref, label)
+    assert read_device_status() == 0
+
+
 def test_fp8_fused_append_flags_and_skips_bad_slots():
     """The one-launch path on an fp8 cache skips and flags new rows whose slot is past the
     table row or in a page outside the pool, like the append kernel."""
