@@ -68,7 +68,9 @@ extern "C" {
                                       and fp8 caches, head_dim 128, an even num_kv_heads >= 8,
                                       2 * seqlen_q * group <= 16, and splits of >= 1024 tokens    */
 #define MX_SCHEDULE_BALANCED_PAIRED 3 /* the balanced schedule over pairs of adjacent KV heads,
-                                      on the same shapes as MX_SCHEDULE_SPLIT_GRID_PAIRED       */
+                                      on the same shapes as MX_SCHEDULE_SPLIT_GRID_PAIRED, and
+                                      on fp8 caches also with 4 or 6 KV heads when the pairs of
+                                      the batch are at least the workgroups                     */
 
 /* Phase flags for mx_paged_gqa_decode (0 = run everything). */
 #define MX_PHASE_MAIN_ONLY 1        /* split grid: run only the split-KV kernel, partials stay in

@@ -2344,6 +2344,11 @@ int query_num_cus(int64_t* num_cus) {
 // (MX_SCHEDULE_SPLIT_GRID_PAIRED, MX_SCHEDULE_BALANCED_PAIRED): calls that allow it (pair_ok:
 // pair_ok_for), head_dim 128, at least 8 KV heads, an even count (token rows of at least 2 KB
 // in bf16, 1 KB in fp8), and both heads' rows in one 16-row tile.
+// pair_ok values (pair_ok_for): no pairs; bf16 rules; fp8 rules, where 4 KV heads (512-byte
+// token rows) also pair on the balanced schedule when there are at least as many pair units as
+// workgroups (a ragged batch: config 4's lengths on an fp8 cache, 63.7-63.9 against 67.5-68.5
+// us; with fewer units, e.g. contest cases 8 and 11 on fp8, pairs lost 16 and 8 %).
+constexpr int kPairNone = 0, kPairBf16 = 1, kPairFp8 = 2;
 bool pair_heads(bool pair_ok, int64_t num_splits, int64_t head_dim, int64_t num_kv_heads,
                 int64_t rows) {
   return pair_ok && num_splits == 0 && head_dim == 128 && num_kv_heads % 2 == 0 &&
@@ -2368,7 +2373,7 @@ int64_t auto_splits(int64_t units, int64_t slots, int64_t cap) {
 
 int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv_heads,
               int64_t head_dim, int64_t page_size, int64_t max_pages, int64_t max_seq_len,
-              int64_t num_splits, int64_t num_cus, bool pair_ok, Plan* plan) {
+              int64_t num_splits, int64_t num_cus, int pair_ok, Plan* plan) {
   if (batch < 1 || seqlen_q < 1 || num_heads < 1 || num_kv_heads < 1 || head_dim < 1 ||
       page_size < 1 || max_pages < 1)
     return fail(MX_STATUS_INVALID_SHAPE,
@@ -2467,7 +2472,11 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
     // ragged lengths with 8 KV heads (B=256, G=4, P=64) 143.0 against 148.5.  With 4 KV heads
     // (1 KB token rows) pairing gained nothing (ragged P=16 82.2 against 81.9, uniform 165.4
     // against 165.9) or lost (config 4, P=64: 84.3 against 80.1), so it needs 2 KB token rows.
-    if (pair_heads(pair_ok, num_splits, head_dim, num_kv_heads, rows)) {
+    const bool narrow_pairs =
+        pair_ok == kPairFp8 && num_kv_heads >= 4 && num_kv_heads % 2 == 0 &&
+        pair_heads(true, num_splits, head_dim, 2 * num_kv_heads, rows) && units / 2 >= groups;
+    if (pair_heads(pair_ok != kPairNone, num_splits, head_dim, num_kv_heads, rows) ||
+        narrow_pairs) {
       plan->schedule = MX_SCHEDULE_BALANCED_PAIRED;
       plan->rows = 2 * rows;
       line_units = units / 2;
@@ -2494,7 +2503,7 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
   // B=4 128K 329.7 against 349.1 us, B=1 128K 91.5 against 94.5, B=4 32K 90.5 against 92.5.
   // Shorter splits lose: B=1 at 32K (512 tokens per paired split) 31.1 against 30.0 us, where
   // the tree's partials of 16 rows lengthen the merge tail.
-  if (pair_heads(pair_ok, num_splits, head_dim, num_kv_heads, rows)) {
+  if (pair_heads(pair_ok != kPairNone, num_splits, head_dim, num_kv_heads, rows)) {
     int64_t ns2 = auto_splits(batch * (num_kv_heads / 2), num_cus * groups_per_cu(head_dim), cap);
     if (ns2 > cap_pages) ns2 = cap_pages;
     if (ns2 < 1) ns2 = 1;
@@ -2620,8 +2629,8 @@ KernelHeads kernel_heads(int64_t seqlen_q, int64_t num_heads, int64_t num_kv_hea
 // without a fused append.  Paired fp8, interleaved A/B against single heads on cold pools:
 // config 2's shape 89.5 and 94.7 against 94.0 and 96.8 us, the B=32 16K sweep 182.4 against
 // 199.7 us, long B=1 128K 54.1 against 55.0, long B=4 32K 53.6 against 53.2.
-bool pair_ok_for(bool fp8, const KernelHeads& kh) {
-  return !fp8 || kh.pair_group == 0;
+int pair_ok_for(bool fp8, const KernelHeads& kh) {
+  return !fp8 ? kPairBf16 : (kh.pair_group == 0 ? kPairFp8 : kPairNone);
 }
 
 // Register ring depth of the fp8 kernels (an fp8 chunk takes half the registers of a bf16 one).
@@ -2867,7 +2876,7 @@ int prepare_decode(const void* q, const void* k_cache, const void* v_cache, cons
                    int64_t head_dim, int64_t page_size, int64_t num_pages,
                    int64_t max_pages_per_seq, int64_t max_seq_len, int32_t causal, float scale,
                    int64_t num_splits, void** workspace, int64_t workspace_bytes,
-                   int32_t phase, void* stream, bool pair_ok, Plan* plan) {
+                   int32_t phase, void* stream, int pair_ok, Plan* plan) {
   if (phase != 0 && phase != MX_PHASE_MAIN_ONLY && phase != MX_PHASE_COMBINE_ONLY)
     return fail(MX_STATUS_INVALID_ARGUMENT, "phase must be 0, 1 or 2");
   // The kernels read q, K and V rows as 16-byte vectors and write out in 8-byte pieces.

@@ -59,20 +59,23 @@ def test_fp8_decode_matches_the_oracle(D, Hq, Hkv, P, ns):
     assert read_device_status() == 0
 
 
-@pytest.mark.parametrize("B,Hq,L,sched,causal", [
-    (16, 32, 4096, "balanced_paired", False),     # config 2's heads: 1 KB fp8 token rows
-    (16, 32, 4096, "balanced_paired", True),      # one token: causal is the same keys
-    (2, 64, 65536, "split_grid_paired", False),   # long context, 32 paired splits of 2 048
+@pytest.mark.parametrize("B,Hq,Hkv,L,sched,causal", [
+    (16, 32, 8, 4096, "balanced_paired", False),     # config 2's heads: 1 KB fp8 token rows
+    (16, 32, 8, 4096, "balanced_paired", True),      # one token: causal is the same keys
+    (2, 64, 8, 65536, "split_grid_paired", False),   # long context, 32 paired splits of 2 048
+    (128, 28, 4, 4096, "balanced_paired", False),    # 4 heads: 256 pair units, 256 groups
+    (16, 28, 4, 4096, "balanced", False),            # 4 heads, fewer pair units than groups
 ])
-def test_fp8_paired_heads_match_the_oracle(B, Hq, L, sched, causal):
-    """fp8 caches with 8 KV heads at head_dim 128 run adjacent heads in pairs, two waves per
-    head, on both schedules; ragged lengths up to the capacity L."""
-    Hkv, D, P = 8, 128, 16
+def test_fp8_paired_heads_match_the_oracle(B, Hq, Hkv, L, sched, causal):
+    """fp8 caches at head_dim 128 run adjacent KV heads in pairs, two waves per head, on both
+    schedules (8 heads), and on the balanced schedule with 4 heads when the pair units are at
+    least the workgroups; ragged lengths up to the capacity L."""
+    D, P = 128, 16
     assert plan(B, Hq, Hkv, D, P, L // P, L, 0, num_cus=256, fp8=True)["schedule"] == sched
     r = random.Random(B + L)
     lens = [L] + [r.randint(1, L) for _ in range(B - 2)] + [r.randint(1, 40)]
     q, k8, v8, table, lt = _case(lens, Hq, Hkv, D, P, seed=L + int(causal))
-    label = f"fp8 paired B={B} Hq={Hq} L={L} {sched} causal={causal}"
+    label = f"fp8 paired B={B} Hq={Hq} Hkv={Hkv} L={L} {sched} causal={causal}"
     print(label, flush=True)
     out = _run(q, k8, v8, table, lt, causal=causal, k_scale=0.8, v_scale=1.2)
     ref = paged_decode_fp8_reference(q, k8, v8, table, lt, k_scale=0.8, v_scale=1.2)
