@@ -1,7 +1,7 @@
 """Benchmark of the paged GQA decode operator on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload llama3_8b]
-                    [--num-splits 0] [--no-cpu-baseline] [--all] [--graph] [--shards N]
+                    [--num-splits 0] [--no-cpu-baseline] [--all] [--no-graph] [--shards N]
 
 One step = one decode-attention call over the whole batch of the workload (default: the
 Llama-3-8B decode shape the metric is quoted on, B=64 Hq=32 Hkv=8 D=128 P=16 L=4096), inputs
@@ -14,7 +14,8 @@ after the second event).  Prints ONE JSON line:
   cpu_baseline  the fp32 oracle (oracle/paged_attention.py) timed on this host on a bounded
              sample of the same workload.
 ``--all`` prints one extra JSON line per north-star configuration (no CPU baseline).
-``--graph`` adds the per-call time of the same calls replayed from a HIP graph.
+The line also carries ``graph_us_per_call``: the same calls captured in a HIP graph and
+replayed, as a serving stack issues them (``--no-graph`` skips it).
 ``--shards N`` prints one extra line: the workload's pages cut into N shards, each shard's
 partial decode and the N-way merge timed on this GPU (the per-GPU work of an N-GPU decode).
 """
@@ -628,8 +629,11 @@ def result_line(args, spec, r, cpu=None) -> dict:
         "wall_ms_per_step": round(r["wall_ms_per_step"], 5),
     }
     if r.get("graph") is not None:
-        # The same calls replayed from a HIP graph (no host launch overhead per call).
+        # The same calls replayed from a HIP graph (no host launch overhead per call), as a
+        # serving stack issues them.
         line["graph"] = r["graph"]
+        line["graph_us_per_call"] = r["graph"]["us_per_call"]
+        line["graph_hbm_frac"] = round(r["graph"]["GBps"] / HBM_PEAK_GBPS, 4)
     if r["warm"] is not None:
         # Cold (the value above: distinct K/V pools rotate, nothing is served from the 256 MB
         # MALL) against warm (one pool reused).
@@ -655,8 +659,11 @@ def main(argv=None) -> int:
     ap.add_argument("--suite", choices=["c500"], default=None,
                     help="run the reference's 14-case contest suite through run_kernel "
                          "instead of the main workload and print its per-case lines and score")
-    ap.add_argument("--graph", action="store_true",
-                    help="also time the calls captured in a HIP graph and replayed")
+    ap.add_argument("--graph", action="store_true", default=True,
+                    help="also time the calls captured in a HIP graph and replayed (default; "
+                         "the line then carries graph_us_per_call)")
+    ap.add_argument("--no-graph", dest="graph", action="store_false",
+                    help="skip the graph-replay timing")
     ap.add_argument("--append-attend", action="store_true",
                     help="time one decode step that appends a new token per sequence: the "
                          "one-launch append-and-attend, the append kernel then the decode, "

@@ -155,10 +155,15 @@ int mx_paged_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
  * MX_NOALLOC_SCRATCH_BYTES is rejected with MX_STATUS_UNSUPPORTED before anything is launched.
  * Every such call on one GPU shares that GPU's array: calls that overlap in time on one GPU
  * (different streams without ordering, or different host threads) race on it, so order them
- * on one stream.  The device status flags of these calls are kept in the array and are not
- * reported through mx_read_device_status.  Returns MX_STATUS_*.
+ * on one stream.  The device status flags of these calls (a bad page id read as page 0, a
+ * sequence clamped to the capacity) go to the array's own status word, which
+ * mx_read_device_status reads when passed MX_NOALLOC_WORKSPACE; it is sticky until read with
+ * reset != 0.  Returns MX_STATUS_*.
  */
 #define MX_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
+/* The workspace argument of mx_read_device_status that names the current device's no-alloc
+ * array (a sentinel, never dereferenced as a host or device address). */
+#define MX_NOALLOC_WORKSPACE ((void*)(intptr_t)-1)
 int mx_paged_gqa_decode_noalloc(const void* q, const void* k_cache, const void* v_cache,
                                 void* out, const int32_t* seq_lens, const int32_t* block_table,
                                 int64_t batch, int64_t seqlen_q, int64_t num_heads,
@@ -349,8 +354,9 @@ int mx_paged_gqa_decode_append_fp8kv(const void* q, const void* k_new, const voi
                                      void* stream);
 
 /* Copies the sticky device status word (MX_DEVICE_* bits) of a workspace (NULL = the library's
- * workspace of the current device) to *flags_out after synchronising the stream; clears it
- * when reset != 0.  Not part of the reference (which validates nothing on the device). */
+ * workspace of the current device, MX_NOALLOC_WORKSPACE = the current device's no-alloc array)
+ * to *flags_out after synchronising the stream; clears it when reset != 0.  Not part of the
+ * reference (which validates nothing on the device). */
 int mx_read_device_status(void* workspace, int32_t reset, void* stream, int32_t* flags_out);
 
 /* Status and message of the last failing call on this host thread (reference has none). */

@@ -79,7 +79,7 @@ constexpr int64_t kPartialBase = kStatusBytes + kCounterBytes;
 // Per-workgroup timeline (profiling builds only)
 // ------------------------------------------------------------------------------------------
 
-// Built with -DMX_WG_TIMELINE (as mx_flash_attn_kernel_opt__amd/timeline.py does), the main
+// Built with -DMX_WG_TIMELINE (a profiling build, never the shipped library), the main
 // kernels record per workgroup (linear id below kTimelineSlots) the wall clock (100 MHz) at
 // entry, at the start of its first streamed piece, at the end of its last one and at exit,
 // plus the XCD it ran on and the number of pieces it streamed; mx_timeline_read copies the
@@ -2271,16 +2271,8 @@ bool split_tree_fits(int64_t units, int64_t splits, int64_t o_bytes) {
 // undercharged, and the workgroups holding many one-chunk units ended last (84 us against a
 // median of 68).  8 took ragged decode from 85.0 to 80.0 us (10 and 12: 81.1, 82.8), the other
 // configurations unchanged.
-#if defined(MX_WG_TIMELINE) && defined(MX_TIMELINE_CHUNK_POSITIONS) && \
-    defined(MX_TIMELINE_UNIT_OVERHEAD)
-// A timeline build may cost the line differently, to compare the workgroup timelines of two
-// line costings from one source.
-constexpr int kChunkPositions = MX_TIMELINE_CHUNK_POSITIONS;
-constexpr int kUnitOverhead = MX_TIMELINE_UNIT_OVERHEAD;
-#else
 constexpr int kChunkPositions = 8;
 constexpr int kUnitOverhead = 8 * kChunkPositions;
-#endif
 static_assert((kChunkPositions & (kChunkPositions - 1)) == 0,
               "the balanced kernels divide by the chunk weight with a shift");
 // Balanced schedule limits: the largest batch whose seq_lens scan stays within two passes of
@@ -2535,8 +2527,8 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
 // Library-owned workspace, one per device, grow-only (as submission_clean.cu:478-491).  A grown
 // workspace never frees its predecessors: kernels still in flight, and HIP graphs captured with
 // the old address, keep valid memory until the process ends.  Growth doubles the size, so the
-// retired allocations add up to less than the current one.  A call that grows it starts a fresh
-// device status word.
+// retired allocations add up to less than the current one (up to 1 GiB; past it growth is to
+// the size needed).  A call that grows it starts a fresh device status word.
 struct DeviceWorkspace {
   void* ptr = nullptr;
   int64_t bytes = 0;
@@ -2565,11 +2557,20 @@ int internal_workspace(int64_t need, hipStream_t stream, void** out) {
       return fail(MX_STATUS_INVALID_ARGUMENT,
                   "the library's workspace must grow, which cannot happen under stream capture: "
                   "pass a workspace, or make one call of this shape before capturing");
-    const int64_t bytes = std::max<int64_t>({need, 2 * ws.bytes, int64_t(1) << 20});
+    // Doubling keeps the retired allocations below the current one; past 1 GiB it stops, and a
+    // failed doubled allocation is retried at exactly `need`.
+    const int64_t grown = ws.bytes < (int64_t(1) << 30) ? 2 * ws.bytes : ws.bytes;
+    int64_t bytes = std::max<int64_t>({need, grown, int64_t(1) << 20});
     void* p = nullptr;
     if (hipMalloc(&p, (size_t)bytes) != hipSuccess || p == nullptr) {
       (void)hipGetLastError();
-      return fail(MX_STATUS_ALLOC_FAILED, "hipMalloc of the internal workspace failed");
+      p = nullptr;
+      if (bytes > need && hipMalloc(&p, (size_t)need) == hipSuccess && p != nullptr) {
+        bytes = need;
+      } else {
+        (void)hipGetLastError();
+        return fail(MX_STATUS_ALLOC_FAILED, "hipMalloc of the internal workspace failed");
+      }
     }
     // status word and merge counters must start at zero
     if (hipMemset(p, 0, (size_t)std::min<int64_t>(bytes, kPartialBase)) != hipSuccess) {
@@ -3111,11 +3112,14 @@ int mx_paged_gqa_decode_noalloc(const void* q, const void* k_cache, const void* 
   if (!q || !k_cache || !v_cache || !out || !seq_lens || !block_table)
     return fail(MX_STATUS_NULL_POINTER,
                 "q, k_cache, v_cache, out, seq_lens and block_table must be non-NULL");
-  // The size check comes first, so a call that cannot run changes nothing on the device.
-  const int64_t need = mx_paged_gqa_decode_workspace_size(
-      batch, seqlen_q, num_heads, num_kv_heads, head_dim, page_size, max_pages_per_seq,
-      max_seq_len, num_splits);
-  if (need < 0) return (int)need;
+  // The size check comes first, so a call that cannot run changes nothing on the device.  It
+  // sizes the bf16 plan that decode_impl runs (not mx_paged_gqa_decode_workspace_size, which
+  // also covers the fp8 plan's kernel heads and can be twice as large at head_dim 64).
+  int64_t need = 0;
+  const int pst = report_plan(false, batch, seqlen_q, num_heads, num_kv_heads, head_dim,
+                              page_size, max_pages_per_seq, max_seq_len, num_splits, 0, nullptr,
+                              nullptr, nullptr, nullptr, &need);
+  if (pst != MX_STATUS_OK) return pst;
   if (need > MX_NOALLOC_SCRATCH_BYTES)
     return fail(MX_STATUS_UNSUPPORTED,
                 "this call needs " + std::to_string(need) +
@@ -3250,7 +3254,11 @@ void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_pa
 int mx_read_device_status(void* workspace, int32_t reset, void* stream, int32_t* flags_out) {
   if (!flags_out) return fail(MX_STATUS_NULL_POINTER, "flags_out must be non-NULL");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (workspace == nullptr) {
+  if (workspace == MX_NOALLOC_WORKSPACE) {
+    // The no-alloc array of this device (cleared on its first use, which may be this one).
+    int st = scratch_address(s, &workspace);
+    if (st != MX_STATUS_OK) return st;
+  } else if (workspace == nullptr) {
     int st = internal_workspace(kStatusBytes, s, &workspace);
     if (st != MX_STATUS_OK) return st;
   }

@@ -463,14 +463,19 @@ class BoundDecodeAppend:
 
 
 def read_device_status(workspace: torch.Tensor | None = None, reset: bool = True,
-                       stream=None, device=None) -> int:
-    """Sticky MX_DEVICE_* bits raised by the kernels (synchronises the stream)."""
+                       stream=None, device=None, noalloc: bool = False) -> int:
+    """Sticky MX_DEVICE_* bits raised by the kernels (synchronises the stream): those of
+    `workspace`, of the library's own workspace (None), or with ``noalloc=True`` those of the
+    device's no-alloc array (the calls of mx_paged_gqa_decode_noalloc)."""
     lib = _lib.load()
+    if noalloc and workspace is not None:
+        raise ValueError("pass either a workspace or noalloc=True")
     dev = workspace.device if workspace is not None else torch.device(
         device if device is not None else "cuda")
     flags = ctypes.c_int32()
+    ws = ctypes.c_void_p(_lib.MX_NOALLOC_WORKSPACE) if noalloc else _ptr(workspace)
     with torch.cuda.device(dev):
-        st = lib.mx_read_device_status(_ptr(workspace), int(bool(reset)),
+        st = lib.mx_read_device_status(ws, int(bool(reset)),
                                        _stream_handle(stream, dev), ctypes.byref(flags))
     _lib.check(st)
     return int(flags.value)

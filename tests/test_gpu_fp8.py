@@ -83,6 +83,25 @@ def test_fp8_paired_heads_match_the_oracle(B, Hq, Hkv, L, sched, causal):
     assert read_device_status() == 0
 
 
+@pytest.mark.parametrize("sq,causal", [(1, False), (2, True)])
+def test_fp8_three_pairs_of_heads(sq, causal):
+    """6 KV heads (512-byte fp8 token rows) pair on the balanced schedule when the 3 pairs per
+    sequence give at least as many pair units as workgroups: an odd pair count per sequence."""
+    B, Hq, Hkv, D, P, L = 96, 12, 6, 128, 16, 4096
+    assert plan(B, Hq, Hkv, D, P, L // P, L, 0, num_cus=256, fp8=True,
+                seqlen_q=sq)["schedule"] == "balanced_paired"
+    r = random.Random(600 + sq)
+    lens = [L, 1, 15, 16, 17, 0] + [r.randint(1, L) for _ in range(B - 6)]
+    q, k8, v8, table, lt = _case(lens, Hq, Hkv, D, P, sq=sq, seed=61 + sq)
+    label = f"fp8 3 pairs sq={sq} causal={causal}"
+    print(label, flush=True)
+    out = _run(q, k8, v8, table, lt, causal=causal, k_scale=0.9, v_scale=1.1)
+    ref = paged_decode_fp8_reference(q, k8, v8, table, lt, k_scale=0.9, v_scale=1.1,
+                                     causal=causal)
+    assert_close_to_oracle(out, ref, label)
+    assert read_device_status() == 0
+
+
 @pytest.mark.parametrize("ns", [0, 3, -5])
 @pytest.mark.parametrize("D,sq,G", [(128, 4, 4), (128, 8, 4), (64, 3, 7), (256, 2, 8)])
 def test_fp8_causal_multi_token_queries(D, sq, G, ns):

@@ -112,9 +112,13 @@ def test_small_query_groups_at_config2_bytes(name):
 
 @pytest.mark.parametrize("name", ["sweep_b32_16k", "sweep_b128_16k", "sweep_d64", "sweep_d256"])
 def test_config5_sweep(name):
+    """Every sequence of each sweep against the oracle (16 sequences' pages on the host at a
+    time), and the device status stays clean."""
     inp = W.make_inputs(name, seed=0, device=DEV)
     out = _decode(inp)
-    _check(inp, out, _sample(inp.spec.batch, 32))         # every sequence of B=32, else 32
+    print(f"{name}: comparing all {inp.spec.batch} sequences", flush=True)
+    _check(inp, out)
+    assert read_device_status() == 0
     del inp
     torch.cuda.empty_cache()
 
@@ -769,6 +773,43 @@ def test_paired_split_grid_partial_outputs():
                                  inp.block_table.cpu(), inp.seq_lens.cpu(), inp.scale)
     assert_close_to_oracle(o.cpu().to(torch.bfloat16), ref, "paired partial o")
     assert torch.isneginf(lse[0]).all().item() and torch.isfinite(lse[1:]).all().item()
+
+
+@pytest.mark.parametrize("Hkv", [10, 12])
+@pytest.mark.parametrize("sched", ["balanced_paired", "split_grid_paired"])
+@pytest.mark.parametrize("sq,causal,partial", [(1, False, False), (2, True, False),
+                                                (1, False, True)])
+def test_paired_odd_and_even_pair_counts(Hkv, sched, sq, causal, partial):
+    """5 and 6 pairs of KV heads (the other paired tests use 2, 4 or 8): the pair index, the
+    unit walk, the slot numbering and the merge counters with an odd pair count, on both paired
+    schedules, with ragged lengths, causal two-token queries and partial outputs; every
+    sequence against the oracle."""
+    from mx_flash_attn_kernel_opt__amd import paged_gqa_decode_partial, plan
+    G = 2
+    if sched == "balanced_paired":
+        g = torch.Generator().manual_seed(Hkv + sq)
+        lens = [0, 1, 15, 16, 17, 1000, 8192] + torch.randint(1, 8193, (41,), generator=g).tolist()
+        cap = 8192
+    else:
+        lens, cap = [32768, 20001, 1], 32768
+    spec = W.custom_spec("pairodd", lens, G * Hkv, Hkv, 128, 16, max_pages=cap // 16,
+                         seqlen_q=sq)
+    inp = W.make_inputs(spec, seed=Hkv * 10 + sq, device=DEV)
+    label = f"Hkv={Hkv} ({Hkv // 2} pairs) {sched} sq={sq} causal={causal} partial={partial}"
+    print(label, flush=True)
+    assert plan(spec.batch, G * Hkv, Hkv, 128, 16, spec.max_pages, seqlen_q=sq)["schedule"] == \
+        sched, label
+    if partial:
+        o, lse = paged_gqa_decode_partial(inp.q, inp.k_cache, inp.v_cache, inp.block_table,
+                                          inp.seq_lens, inp.scale, causal=causal)
+        torch.cuda.synchronize()
+        out = o.to(torch.bfloat16)
+        assert torch.isfinite(lse[torch.as_tensor(lens) > 0]).all().item(), label
+    else:
+        out = _decode(inp, causal=causal).clone()
+        assert torch.equal(_decode(inp, causal=causal), out), label
+    _mq_check(inp, out, causal, label)
+    assert read_device_status() == 0, label
 
 
 # ------------------------------------------------------------------------------------------

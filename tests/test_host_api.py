@@ -261,6 +261,37 @@ def test_paired_split_grid_plan(B, Hq, Hkv, D, cap, sq, fp8, ns_req, sched, spli
         assert p["tokens_per_split"] >= 1024
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,cap,sq,fp8,sched,units", [
+    (48, 20, 10, 8192, 1, False, "balanced_paired", 240),   # 5 pairs per sequence
+    (48, 40, 10, 8192, 2, False, "balanced_paired", 240),   # 2 tokens x group 4 x 2 heads
+    (2, 20, 10, 32768, 1, False, "split_grid_paired", 10),
+    (2, 40, 10, 32768, 2, False, "split_grid_paired", 10),
+    (48, 24, 12, 8192, 1, False, "balanced_paired", 288),   # 6 pairs
+    (2, 24, 12, 32768, 1, False, "split_grid_paired", 12),
+    (96, 12, 6, 4096, 1, True, "balanced_paired", 288),     # fp8, 3 pairs of 512-byte rows
+    (128, 24, 6, 4096, 2, True, "balanced_paired", 384),
+    (96, 12, 6, 4096, 1, False, "balanced", 576),           # bf16 1.5 KB rows: not paired
+    (40, 24, 6, 4096, 1, True, "balanced", 240),            # fp8: fewer pair units than groups
+])
+def test_odd_pair_counts_plan(B, Hq, Hkv, cap, sq, fp8, sched, units):
+    """Automatic plans over an odd number of KV-head pairs per sequence (5 or 3) and an even
+    one (6): paired units are B * Hkv / 2, with both heads' rows in one slot; the balanced
+    plan's slots are one per workgroup and one per unit."""
+    p = plan(B, Hq, Hkv, 128, 16, cap // 16, cap, 0, num_cus=256, seqlen_q=sq, fp8=fp8)
+    assert p["schedule"] == sched
+    paired = sched.endswith("_paired")
+    assert units == B * (Hkv // 2 if paired else Hkv)
+    if sched.startswith("balanced"):
+        assert p["workgroups"] == 256
+        rows = sq * Hq // Hkv * (2 if paired else 1)
+        slots = 256 + units
+        o_off = PARTIAL_BASE + math.ceil(slots * rows * 4 / 256) * 256
+        assert p["workspace_bytes"] == o_off + slots * rows * 128 * 4
+    else:
+        assert p["workgroups"] == units * p["splits"] and p["tokens_per_split"] >= 1024
+        assert p["launches"] == 1
+
+
 @pytest.mark.parametrize("B,Hkv,cap,sched,splits", [
     (64, 8, 64, "split_grid", 1),       # short capacity: one split per unit, no merge
     (64, 8, 512, "split_grid", 1),
