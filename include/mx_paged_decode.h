@@ -53,6 +53,9 @@ extern "C" {
 /* Bits of the device status word (sticky; read with mx_read_device_status). */
 #define MX_DEVICE_BAD_PAGE_ID 1u    /* a valid block_table slot held an id outside [0, num_pages) */
 #define MX_DEVICE_SEQ_TOO_LONG 2u   /* seq_lens[b] exceeded the capacity the call was planned for */
+#define MX_DEVICE_WORKSPACE_STATE 4u /* the workspace's counter region was not zero at launch (a
+                                        workspace not zero-filled, or shared by overlapping calls):
+                                        that call's output is not valid                         */
 
 /* Schedules reported by mx_paged_gqa_decode_plan. */
 #define MX_SCHEDULE_SPLIT_GRID 0   /* grid (Hkv * row groups, batch, splits); the splits of
@@ -123,9 +126,9 @@ void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_pa
  *                      number of pages of max_seq_len);
  *                      < 0 = balanced schedule with exactly -num_splits workgroups.
  *   workspace          device memory of >= mx_paged_gqa_decode_workspace_size() bytes,
- *                      zero-filled once by the caller before first use (its first 196 864
- *                      bytes hold a status word and merge counters that every call leaves at
- *                      zero); NULL = library-owned: one per device, grown on demand
+ *                      zero-filled once by the caller before first use (its first 229 632
+ *                      bytes hold a status word, workgroup claim masks and merge counters
+ *                      that every call leaves at zero); NULL = library-owned: one per device, grown on demand
  *                      (doubling; earlier allocations are kept, never freed, so graphs
  *                      captured with them stay valid).  A call that needs it to grow fails
  *                      with MX_STATUS_INVALID_ARGUMENT on a capturing stream.

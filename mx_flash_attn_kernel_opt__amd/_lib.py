@@ -26,6 +26,7 @@ MX_STATUS_INVALID_ARGUMENT = -7
 
 MX_DEVICE_BAD_PAGE_ID = 1
 MX_DEVICE_SEQ_TOO_LONG = 2
+MX_DEVICE_WORKSPACE_STATE = 4
 # mx_read_device_status's workspace sentinel for the no-alloc array ((void*)(intptr_t)-1).
 MX_NOALLOC_WORKSPACE = ctypes.c_void_p(-1).value
 

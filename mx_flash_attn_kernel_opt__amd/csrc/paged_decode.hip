@@ -69,11 +69,17 @@ constexpr float kRescaleSlack = 8.0f;  // log2 units the stale running max may l
 // workspace keeps valid counters across calls of any shape, whatever the partials of earlier
 // calls left behind.
 constexpr int kStatusBytes = 256;
+// XCD claim masks (xcd_slot): one 32-bit word per block of 8 workgroups, each in a 256-byte line
+// of its own, so the claims of different blocks never contend for one line (packed into one
+// line, 256 claims serialised and took config 2 from 156 to 165 us).
+constexpr int kXcdMaskWords = 128;
+constexpr int kXcdMaskStride = 64;  // words
+constexpr int64_t kXcdMaskBytes = (int64_t)kXcdMaskWords * kXcdMaskStride * 4;
 constexpr int kMaxSlots = 4096 + 8192;          // balanced: workgroups + batch * Hkv
 constexpr int kBalancedBatch = 512;             // balanced: largest batch
 constexpr int kCounterLevels = 4;               // fan-in-8 merge tree levels
 constexpr int64_t kCounterBytes = (int64_t)kCounterLevels * kMaxSlots * 4;
-constexpr int64_t kPartialBase = kStatusBytes + kCounterBytes;
+constexpr int64_t kPartialBase = kStatusBytes + kXcdMaskBytes + kCounterBytes;
 
 // ------------------------------------------------------------------------------------------
 // Per-workgroup timeline (profiling builds only)
@@ -160,6 +166,45 @@ __device__ __forceinline__ float group_sum4(float x) {
 
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 
+// XCD-stable workgroup order (thread 0 calls it; the caller hands the result to the workgroup).
+// The dispatcher deals a launch's workgroups to the 8 XCDs in turn, starting at the XCD after
+// the one its hardware queue dispatched to last, so the XCD of workgroup w varies between
+// launches (eager calls back to back, graph replays, calls after other kernels).  A workgroup's
+// streaming rate depends on its XCD and on the byte offsets of the rows it streams, so one
+// mapping of shares to XCDs runs measurably faster than its rotations (config 2: 156 against
+// 162-164 us).  xcd_slot fixes the mapping: workgroup w of the aligned block k = w / 8 takes
+// logical index 8k + x, x its own XCC_ID, by claiming bit x of the block's mask word
+// (atomicOr); when another workgroup of the block holds that bit (a block the dispatcher did
+// not deal one to each XCD), it claims the first free bit.  The block's 8 workgroups claim 8
+// distinct bits, so the mapping is a bijection whatever the dispatch; the claim that fills the
+// mask clears it, when no other claim of the block is left, for the next launch.  Workgroups of
+// a last, partial block keep their own index.  Relaxed agent-scope atomics: the mask only
+// arbitrates indices, nothing is published through it.  The masks start at zero like the merge
+// counters (a zero-filled workspace, each launch leaving them zero); were one not, a claim could
+// find no free bit: xcd_slot then returns -1 and the kernel raises MX_DEVICE_WORKSPACE_STATE.
+__device__ __forceinline__ int xcd_slot(int w, int n, uint32_t* masks) {
+  const int k = w >> 3;
+  if ((k + 1) * 8 > n) return w;
+  unsigned xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  int slot = (int)(xcc & 7u);
+  uint32_t bit = 1u << slot;
+  uint32_t* m = masks + k * kXcdMaskStride;
+  uint32_t old = __hip_atomic_fetch_or(m, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (old & bit) {
+    // Taken: the first free bit (one exists: the block has 8 workgroups for 8 bits).
+    for (slot = 0; slot < 8; ++slot) {
+      bit = 1u << slot;
+      if (old & bit) continue;
+      old = __hip_atomic_fetch_or(m, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (!(old & bit)) break;
+    }
+    if (slot == 8) return -1;
+  }
+  if ((old | bit) == 0xffu) __hip_atomic_store(m, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return 8 * k + slot;
+}
+
 // Round-to-nearest-even pack of two floats into one dword of bf16 (lo in bits 0..15).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   const f32x2 f = {lo, hi};
@@ -225,6 +270,22 @@ __device__ __forceinline__ void load_v_row(uint32_t (&dst)[D / 32], const uint16
       dst[w + 3] = x[3];
     }
   }
+}
+
+// A load from a wave-uniform address of memory no kernel of the launch writes (the block table),
+// made a scalar load: the address goes through SGPRs (readfirstlane) and is read through the
+// constant address space, whatever registers the compiler gave its operands.  The page ids of
+// the chunk stream must stay scalar loads: issued as vector loads behind the other ring slot's
+// K/V loads and waited for before the refill, they serialise the ring (a register allocation
+// that did that took config 2 from 156 to 164 us and head_dim 64 from 163 to 193 us).
+typedef const int32_t __attribute__((address_space(4))) ConstInt32;
+__device__ __forceinline__ int scalar_load(const int32_t* p) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  // (readfirstlane returns an int: each half goes through uint32_t, so the low half is
+  // zero-extended, never sign-extended into the high one.)
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  return *reinterpret_cast<ConstInt32*>(((uint64_t)hi << 32) | (uint64_t)lo);
 }
 
 // Per-lane byte offsets of a chunk inside its page (constant for the whole wave).
@@ -533,6 +594,7 @@ struct MainShape {
   int num_splits;
   int tokens_per_split;  // multiple of page_size
   int fused_combine;     // split grid: the splits of each unit merge their partials in-kernel
+  int xcd_map;           // workgroups take XCD-stable indices (xcd_slot) instead of blockIdx
   int split_groups;      // split grid: ceil(num_splits / kMergeFanIn), merge counters per unit
   // balanced schedule
   int num_groups;        // workgroups of the launch
@@ -707,8 +769,11 @@ __device__ __forceinline__ void stream_chunks(SoftmaxState<D> (&st)[KT],
 
   // Element offset of chunk c (16 tokens) inside the K/V pools.  Only table entries below
   // ceil(seq / page_size) are ever read.
+  // (c is below c_hi wherever a chunk is loaded; clamping the index to the stream's last chunk
+  // keeps the load's address a valid table entry however the compiler schedules it.)
+  const int c_top = max(c_hi - 1, 0);
   auto chunk_base = [&](int c) -> int64_t {
-    int pid = bt_row[c >> sh.chunk_shift];
+    int pid = scalar_load(bt_row + (min(c, c_top) >> sh.chunk_shift));
     if (pid < 0 || (sh.num_pages > 0 && pid >= sh.num_pages)) {
       bad_page = true;
       pid = 0;
@@ -1729,7 +1794,7 @@ void mx_paged_decode_balanced(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wg = blockIdx.x;
+  const int wg0 = blockIdx.x;                        // dispatch index (see wg below)
   const int TR = sh.tile_rows;                       // rows per partial slot
   const int UPS = sh.num_kv_heads * sh.row_tiles;    // units per sequence
   const int B = sh.batch;
@@ -1747,7 +1812,7 @@ void mx_paged_decode_balanced(
     const int b = tid * kScanPerThread + i;
     const int len = b < B ? seq_lens[b] : 0;
     if (b < B) s_len[b] = len;
-    const int seq = b < B ? seq_extent_of<kAppend>(len, sh, status, wg == 0).sched : 0;
+    const int seq = b < B ? seq_extent_of<kAppend>(len, sh, status, wg0 == 0).sched : 0;
     wts[i] = seq > 0 ? (seq + kChunk - 1) / kChunk : 0;
     if (b < B) {
       nb_lo = min(nb_lo, wts[i]);
@@ -1795,15 +1860,31 @@ void mx_paged_decode_balanced(
     wts[i] = wts[i] > 0 ? UPS * (wts[i] * wc + alpha) : 0;
     mine += wts[i];
   }
+  // This workgroup's index on the line: XCD-stable (xcd_slot) in the paired kernels, claimed
+  // after the seq_lens loads so the claim's round trip overlaps the scan.  (Only there: the claim
+  // code, even switched off, changed the other kernels' register allocation and cost them 1-2 %,
+  // and only the paired units showed the placement effect in measurements.)
+  if constexpr (kPairW) {
+    if (tid == 0)
+      s_int[NW + 3] = sh.xcd_map ? xcd_slot(wg0, sh.num_groups, status + kStatusBytes / 4) : wg0;
+  }
   // One scan over the workgroup: positions before this thread's first sequence, and the total.
   const int incl = wave_inclusive_sum(mine);
   if (tid == 0) s_int[NW] = -1;
   if (lane == 63) s_int[wv] = incl;
   __syncthreads();
+  int wg = wg0;
+  if constexpr (kPairW) {
+    wg = __builtin_amdgcn_readfirstlane(s_int[NW + 3]);
+    if (wg < 0) {  // the claim masks were not zero (see xcd_slot)
+      if (tid == 0) atomicOr(status, (uint32_t)MX_DEVICE_WORKSPACE_STATE);
+      wg = wg0;
+    }
+  }
   // Empty sequences (L <= 0) are defined as zero output; sequence b's zeros (its seqlen_q *
   // num_heads consecutive rows) are written by workgroup b % num_groups.
   if constexpr (!kAppend) {
-    for (int b = wg; b < B; b += sh.num_groups) {
+    for (int b = wg0; b < B; b += sh.num_groups) {
       if (key_count_of(s_len[b], sh.appended) <= 0) {
         const int64_t row0 = (int64_t)b * sh.seqlen_q * sh.num_heads;
         for (int e = tid; e < sh.seqlen_q * sh.num_heads * (D / 4); e += 64 * NW)
@@ -2476,7 +2557,7 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
     }
     plan->slots = groups + line_units;
     plan->cap_tokens = cap;
-    plan->counter_offset = kStatusBytes;
+    plan->counter_offset = kStatusBytes + kXcdMaskBytes;
     plan->lse_offset = kPartialBase;
     plan->o_offset = plan->lse_offset + align_up(plan->slots * slot_rows * 4, 256);
     plan->workspace_bytes = plan->o_offset + plan->slots * slot_rows * head_dim * 4;
@@ -2681,6 +2762,9 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   sh.num_splits = (int)plan.splits;
   sh.fused_combine = 0;
   sh.split_groups = 1;
+  // Paired balanced launches take XCD-stable shares (xcd_slot) when their blocks of 8
+  // workgroups fit the claim masks.
+  sh.xcd_map = plan.schedule == MX_SCHEDULE_BALANCED_PAIRED && plan.groups <= 8 * kXcdMaskWords;
   sh.tokens_per_split = (int)plan.tokens_per_split;
   sh.num_groups = (int)plan.groups;
   // A paired unit's chunk holds two heads' rows: twice a single head's weight on the line.
@@ -2754,7 +2838,8 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
     auto go = [&](auto kernel, auto kc, auto vc) {
       hipLaunchKernelGGL(kernel, grid, dim3(64 * kNW), 0, stream, q16, kc, vc,
                          static_cast<uint16_t*>(out), seq_lens, block_table, part_o, part_lse,
-                         reinterpret_cast<uint32_t*>(ws + kStatusBytes), status, sh);
+                         reinterpret_cast<uint32_t*>(ws + kStatusBytes + kXcdMaskBytes), status,
+                         sh);
     };
     if (paired) {
       // make_plan pairs only head_dim 128 with one tile.

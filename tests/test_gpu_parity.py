@@ -414,6 +414,35 @@ def test_bad_page_id_is_flagged_not_read(ns):
     _check(inp, out, batches=[0], label="unaffected sequence")
 
 
+def test_claim_mask_left_set_is_flagged_and_output_stays_valid():
+    """The paired balanced kernel gives workgroups XCD-stable indices by claiming bits of one
+    mask word per block of 8 workgroups (the workspace's bytes 256 .. 260 for block 0).  A mask
+    that is not zero at launch (a workspace not zero-filled) makes that block's claims fail:
+    the kernel flags MX_DEVICE_WORKSPACE_STATE and those workgroups keep their own indices, so
+    here (every other block claims normally) the output is still every row against the
+    oracle."""
+    from mx_flash_attn_kernel_opt__amd import _lib, plan
+    spec = W.custom_spec("claim", [4096, 100, 17, 2049] * 16, 32, 8, 128, 16)
+    inp = W.make_inputs(spec, seed=23, device=DEV)
+    p = plan(spec.batch, 32, 8, 128, 16, spec.max_pages)
+    assert p["schedule"] == "balanced_paired"
+    ws = torch.zeros(p["workspace_bytes"], dtype=torch.uint8, device=DEV)
+    ws[256] = 0xFF                         # block 0's mask: every bit already claimed
+    out = paged_gqa_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_table, inp.seq_lens,
+                           inp.scale, workspace=ws)
+    torch.cuda.synchronize()
+    assert read_device_status(ws) == _lib.MX_DEVICE_WORKSPACE_STATE
+    _check(inp, out, label="claim mask left set")
+    assert ws[256].item() == 0xFF          # no claim completed it, so none cleared it
+    ws[256] = 0
+    again = paged_gqa_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_table, inp.seq_lens,
+                             inp.scale, workspace=ws)
+    torch.cuda.synchronize()
+    assert read_device_status(ws) == 0
+    assert torch.equal(again, out)
+    assert not ws[256:256 + 128 * 256].any().item()   # every mask back at zero
+
+
 def test_run_kernel_bounds_page_ids_by_num_blocks():
     """run_kernel takes num_blocks as the pool size (task.md:57-58): an id in a valid slot at or
     past num_blocks is flagged and read as page 0.  The tensors hold 16 pages, more than the

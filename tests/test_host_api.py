@@ -64,7 +64,7 @@ def test_run_kernel_abi_matches_the_reference_binding():
 # ------------------------------------------------------------------------------------------
 
 FAKE = ctypes.c_void_p(0x1000)   # never dereferenced: validation fails first
-PARTIAL_BASE = 256 + 4 * (4096 + 8192) * 4   # status word + fixed merge-counter region
+PARTIAL_BASE = 256 + 128 * 256 + 4 * (4096 + 8192) * 4   # status word, XCD claim masks, merge counters
 
 
 def _decode(**over):
