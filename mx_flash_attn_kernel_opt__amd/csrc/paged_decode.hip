@@ -1826,6 +1826,7 @@ void mx_paged_decode_balanced(
   // pieces longer, and shares that straddle units would pay two pieces).
   int alpha = sh.unit_overhead;
   int wc = sh.chunk_weight;
+  int equal_k = 0;  // k when every unit is cut into k equal pieces, one per share
   const int units = B * UPS;
   // (k = 1 needs no change: every workgroup then holds one whole unit whatever the charge.)
   if (sh.num_groups > units && sh.num_groups % units == 0) {  // the same in every thread
@@ -1852,6 +1853,7 @@ void mx_paged_decode_balanced(
       const int k = sh.num_groups / units;
       wc = 1;
       alpha = (k - nb_lo % k) % k;
+      equal_k = k;
     }
   }
   int mine = 0;
@@ -1881,6 +1883,10 @@ void mx_paged_decode_balanced(
       wg = wg0;
     }
   }
+  // Equal pieces: consecutive workgroups take the same piece of consecutive units (as the split
+  // grid's consecutive workgroups take consecutive KV heads), not the k pieces of one unit.
+  // Uniform B=8-16, L=4096 batches: 1-3 % faster.
+  if (equal_k > 0) wg = (wg % units) * equal_k + wg / units;
   // Empty sequences (L <= 0) are defined as zero output; sequence b's zeros (its seqlen_q *
   // num_heads consecutive rows) are written by workgroup b % num_groups.
   if constexpr (!kAppend) {

@@ -17,6 +17,7 @@ the GPU; cases above ``CPU_GEN_LIMIT`` elements draw on the target device's gene
 from __future__ import annotations
 
 import math
+import re
 from dataclasses import dataclass, field, replace
 
 import torch
@@ -196,6 +197,26 @@ def c500_spec(case: int, table: str = "arange") -> DecodeSpec:
                       table=table, description=f"contest case {case}: b{batch} cap{cap} kv{kv}")
 
 
+_SHAPE_NAME = re.compile(r"(uniform|ragged)_b(\d+)_hq(\d+)_hkv(\d+)_l(\d+)")
+
+
+def shape_spec(kind: str, batch: int, num_heads: int, num_kv_heads: int, length: int) -> DecodeSpec:
+    """Head_dim 128, page_size 16 decode of `batch` sequences: every one `length` keys
+    ("uniform"), or config 4's recipe up to `length` ("ragged": log-uniform in [1, length], 10 %
+    in [1, 15])."""
+    pages = math.ceil(length / 16)
+    name = f"{kind}_b{batch}_hq{num_heads}_hkv{num_kv_heads}_l{length}"
+    if kind == "uniform":
+        return DecodeSpec(name, batch, num_heads, num_kv_heads, 128, 16, pages, "fixed", (length,),
+                          description=f"uniform B={batch} Hq={num_heads} Hkv={num_kv_heads} L={length}")
+    if kind == "ragged":
+        return DecodeSpec(name, batch, num_heads, num_kv_heads, 128, 16, pages, "loguniform_ragged",
+                          (1, length, 0.10, 15),
+                          description=f"ragged B={batch} Hq={num_heads} Hkv={num_kv_heads} "
+                                      f"L log-uniform [1,{length}], 10% in [1,15]")
+    raise ValueError(f"unknown shape kind {kind!r}")
+
+
 def get_spec(name: str) -> DecodeSpec:
     if name in NORTH_STAR:
         return NORTH_STAR[name]
@@ -203,7 +224,11 @@ def get_spec(name: str) -> DecodeSpec:
         return EXTRA[name]
     if name.startswith("c500_case"):
         return c500_spec(int(name[len("c500_case"):]))
-    raise KeyError(f"unknown workload {name!r}; known: {sorted(NORTH_STAR)} and c500_case1..14")
+    m = _SHAPE_NAME.fullmatch(name)
+    if m:
+        return shape_spec(m.group(1), *(int(x) for x in m.groups()[1:]))
+    raise KeyError(f"unknown workload {name!r}; known: {sorted(NORTH_STAR)}, c500_case1..14, "
+                   "uniform_bB_hqH_hkvK_lL and ragged_bB_hqH_hkvK_lL")
 
 
 # ---------------------------------------------------------------------------------------

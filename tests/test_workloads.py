@@ -70,6 +70,20 @@ def test_ragged_recipe():
     assert len(set(table.flatten().tolist())) == 256 * 128
 
 
+def test_named_shapes():
+    u = W.get_spec("uniform_b16_hq32_hkv8_l4096")
+    assert (u.batch, u.num_heads, u.num_kv_heads, u.head_dim, u.page_size) == (16, 32, 8, 128, 16)
+    assert u.capacity == 4096
+    lens = W.make_inputs(u, seed=3).seq_lens
+    assert lens.tolist() == [4096] * 16
+    r = W.get_spec("ragged_b8_hq64_hkv8_l8192")
+    assert (r.batch, r.num_heads, r.num_kv_heads, r.capacity) == (8, 64, 8, 8192)
+    lens = W.make_inputs(r, seed=3).seq_lens
+    assert int(lens.min()) >= 1 and int(lens.max()) <= 8192 and len(set(lens.tolist())) > 1
+    with pytest.raises(KeyError):
+        W.get_spec("uniform_b16_hq32_l4096")
+
+
 @pytest.mark.parametrize("case", range(1, 15))
 def test_c500_case_recipe(case):
     spec = W.c500_spec(case)
