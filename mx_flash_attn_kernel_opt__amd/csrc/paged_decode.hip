@@ -1621,15 +1621,35 @@ void mx_paged_decode_splitkv(
   // Wave index, made provably wave-uniform so the chunk indices derived from it stay in
   // SGPRs and the page lookups remain scalar loads (off the vector-memory counter).
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kv = sh.row_tiles == 1 ? (int)blockIdx.x : (int)blockIdx.x / sh.row_tiles;
-  const int grp = blockIdx.x - kv * sh.row_tiles;  // row group: rows grp*16*KT ..
+  // Grid position (unit of the sequence, sequence, split).  Paired launches take XCD-stable
+  // positions (xcd_slot, as the paired balanced kernel): the claim's round trip overlaps the
+  // length load, and its barrier comes before any other use of s_last.
+  int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+  if constexpr (kPairW) {
+    if (sh.xcd_map) {
+      const int X = gridDim.x, Y = gridDim.y;
+      const int w0 = bx + X * (by + Y * bz);
+      if (tid == 0) s_last = xcd_slot(w0, X * Y * (int)gridDim.z, status + kStatusBytes / 4);
+      __syncthreads();
+      int w = __builtin_amdgcn_readfirstlane(s_last);
+      if (w < 0) {  // the claim masks were not zero (see xcd_slot)
+        if (tid == 0) atomicOr(status, (uint32_t)MX_DEVICE_WORKSPACE_STATE);
+        w = w0;
+      }
+      bx = w % X;
+      by = (w / X) % Y;
+      bz = w / (X * Y);
+    }
+  }
+  const int kv = sh.row_tiles == 1 ? bx : bx / sh.row_tiles;
+  const int grp = bx - kv * sh.row_tiles;  // row group: rows grp*16*KT ..
   const int r0 = grp * 16 * KT;
-  const int b = blockIdx.y;
-  const int split = blockIdx.z;
+  const int b = by;
+  const int split = bz;
   const int nrows = min(16 * KT, sh.rows - r0);  // query rows of this group
 
   const SeqExtent ext =
-      seq_extent<kAppend>(seq_lens, b, sh, status, split == 0 && blockIdx.x == 0 && tid == 0);
+      seq_extent<kAppend>(seq_lens, b, sh, status, split == 0 && bx == 0 && tid == 0);
   const int seq = ext.sched;
   if (ext.keys <= 0) {
     // Empty sequence: defined as a zero output.
@@ -1722,7 +1742,7 @@ void mx_paged_decode_splitkv(
   // This split's partial is level-0 item `split` of the unit's merge tree.
   const int nsv = (seq + sh.tokens_per_split - 1) / sh.tokens_per_split;  // splits with tokens
   const SplitTree<D> tree{sh,  part_o, part_lse, counters, out, row_base(b, kv, sh), r0,
-                          b * (int)gridDim.x + (int)blockIdx.x};
+                          b * (int)gridDim.x + bx};
   merge_tree<D, NW, kMergeFanIn>(tree, split, nsv, nrows, s_lse, &s_last);
   copy_if_writer();
 }
@@ -2768,9 +2788,12 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   sh.num_splits = (int)plan.splits;
   sh.fused_combine = 0;
   sh.split_groups = 1;
-  // Paired balanced launches take XCD-stable shares (xcd_slot) when their blocks of 8
-  // workgroups fit the claim masks.
-  sh.xcd_map = plan.schedule == MX_SCHEDULE_BALANCED_PAIRED && plan.groups <= 8 * kXcdMaskWords;
+  // Paired launches (balanced and split grid) take XCD-stable shares or grid positions
+  // (xcd_slot) when their blocks of 8 workgroups fit the claim masks.
+  sh.xcd_map =
+      (plan.schedule == MX_SCHEDULE_BALANCED_PAIRED && plan.groups <= 8 * kXcdMaskWords) ||
+      (plan.schedule == MX_SCHEDULE_SPLIT_GRID_PAIRED &&
+       batch * kernel_kv * plan.row_tiles * plan.splits <= 8 * kXcdMaskWords);
   sh.tokens_per_split = (int)plan.tokens_per_split;
   sh.num_groups = (int)plan.groups;
   // A paired unit's chunk holds two heads' rows: twice a single head's weight on the line.

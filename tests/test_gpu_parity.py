@@ -443,6 +443,33 @@ def test_claim_mask_left_set_is_flagged_and_output_stays_valid():
     assert not ws[256:256 + 128 * 256].any().item()   # every mask back at zero
 
 
+def test_split_grid_claim_mask_left_set_is_flagged_and_output_stays_valid():
+    """The paired split grid takes XCD-stable grid positions through the same claim masks as
+    the paired balanced kernel.  Block 0's mask set at launch: its claims fail, the kernel flags
+    MX_DEVICE_WORKSPACE_STATE and those workgroups keep their own grid positions, so the output
+    still matches the oracle; with the mask cleared the call is clean and bitwise equal."""
+    from mx_flash_attn_kernel_opt__amd import _lib, plan
+    spec = W.custom_spec("claim_sg", [65536], 64, 8, 128, 16)
+    inp = W.make_inputs(spec, seed=24, device=DEV)
+    p = plan(spec.batch, 64, 8, 128, 16, spec.max_pages)
+    assert p["schedule"] == "split_grid_paired" and p["workgroups"] == 256
+    ws = torch.zeros(p["workspace_bytes"], dtype=torch.uint8, device=DEV)
+    ws[256] = 0xFF
+    out = paged_gqa_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_table, inp.seq_lens,
+                           inp.scale, workspace=ws)
+    torch.cuda.synchronize()
+    assert read_device_status(ws) == _lib.MX_DEVICE_WORKSPACE_STATE
+    _check(inp, out, label="split grid claim mask left set")
+    assert ws[256].item() == 0xFF
+    ws[256] = 0
+    again = paged_gqa_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_table, inp.seq_lens,
+                             inp.scale, workspace=ws)
+    torch.cuda.synchronize()
+    assert read_device_status(ws) == 0
+    assert torch.equal(again, out)
+    assert not ws[256:256 + 128 * 256].any().item()
+
+
 def test_run_kernel_bounds_page_ids_by_num_blocks():
     """run_kernel takes num_blocks as the pool size (task.md:57-58): an id in a valid slot at or
     past num_blocks is flagged and read as page 0.  The tensors hold 16 pages, more than the
