@@ -1794,7 +1794,7 @@ struct BalancedTree {
 // as in mx_paged_decode_splitkv with kPairW (waves 0-1 the first head, 2-3 the second), and a
 // pair's chunk weighs twice a single head's on the line (MainShape::chunk_weight).
 template <int D, int NBUF, int NW, bool kCausal, int KT, bool kAppend, bool kFp8,
-          bool kPairW = false>
+          bool kPairW = false, bool kXcdMap = kPairW>
 __global__ __launch_bounds__(64 * NW)
 __attribute__((amdgpu_waves_per_eu(min_waves_per_simd<D, KT>())))
 void mx_paged_decode_balanced(
@@ -1886,7 +1886,7 @@ void mx_paged_decode_balanced(
   // after the seq_lens loads so the claim's round trip overlaps the scan.  (Only there: the claim
   // code, even switched off, changed the other kernels' register allocation and cost them 1-2 %,
   // and only the paired units showed the placement effect in measurements.)
-  if constexpr (kPairW) {
+  if constexpr (kXcdMap) {
     if (tid == 0)
       s_int[NW + 3] = sh.xcd_map ? xcd_slot(wg0, sh.num_groups, status + kStatusBytes / 4) : wg0;
   }
@@ -1896,7 +1896,7 @@ void mx_paged_decode_balanced(
   if (lane == 63) s_int[wv] = incl;
   __syncthreads();
   int wg = wg0;
-  if constexpr (kPairW) {
+  if constexpr (kXcdMap) {
     wg = __builtin_amdgcn_readfirstlane(s_int[NW + 3]);
     if (wg < 0) {  // the claim masks were not zero (see xcd_slot)
       if (tid == 0) atomicOr(status, (uint32_t)MX_DEVICE_WORKSPACE_STATE);
@@ -2793,7 +2793,9 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   sh.xcd_map =
       (plan.schedule == MX_SCHEDULE_BALANCED_PAIRED && plan.groups <= 8 * kXcdMaskWords) ||
       (plan.schedule == MX_SCHEDULE_SPLIT_GRID_PAIRED &&
-       batch * kernel_kv * plan.row_tiles * plan.splits <= 8 * kXcdMaskWords);
+       batch * kernel_kv * plan.row_tiles * plan.splits <= 8 * kXcdMaskWords) ||
+      (plan.schedule == MX_SCHEDULE_BALANCED && D == 128 && seqlen_q > 1 && !kv.fp8 &&
+       app.new_tokens == 0 && plan.groups <= 8 * kXcdMaskWords);
   sh.tokens_per_split = (int)plan.tokens_per_split;
   sh.num_groups = (int)plan.groups;
   // A paired unit's chunk holds two heads' rows: twice a single head's weight on the line.
@@ -2847,7 +2849,13 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
       go(mx_paged_decode_balanced<D, kNBUF8, kNW, kCausal, KT, false, true>, k8, v8);
     else if (append)
       go(mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, true, false>, k16, v16);
-    else
+    else if (sh.xcd_map) {
+      if constexpr (D == 128)
+        go(mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, false, false, false, true>, k16,
+           v16);
+      else
+        return hipErrorInvalidValue;
+    } else
       go(mx_paged_decode_balanced<D, kNBUF, kNW, kCausal, KT, false, false>, k16, v16);
     return hipGetLastError();
   }

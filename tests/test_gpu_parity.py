@@ -470,6 +470,36 @@ def test_split_grid_claim_mask_left_set_is_flagged_and_output_stays_valid():
     assert not ws[256:256 + 128 * 256].any().item()
 
 
+def test_multi_token_claim_mask_left_set_is_flagged_and_output_stays_valid():
+    """Multi-token queries at head_dim 128 run the single-head balanced kernel with XCD-stable
+    shares (the same claim masks).  Block 0's mask set at launch is flagged, the output still
+    matches the oracle, and the next call with the mask cleared is clean and bitwise equal."""
+    from mx_flash_attn_kernel_opt__amd import _lib, plan
+    spec = W.custom_spec("claim_mt", [4096, 333, 1, 2048] * 4, 32, 8, 128, 16, seqlen_q=4,
+                         causal=True)
+    inp = W.make_inputs(spec, seed=25, device=DEV)
+    p = plan(spec.batch, 32, 8, 128, 16, spec.max_pages, seqlen_q=4)
+    assert p["schedule"] == "balanced"
+    ws = torch.zeros(p["workspace_bytes"], dtype=torch.uint8, device=DEV)
+    ws[256] = 0xFF
+    out = paged_gqa_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_table, inp.seq_lens,
+                           inp.scale, causal=True, workspace=ws)
+    torch.cuda.synchronize()
+    assert read_device_status(ws) == _lib.MX_DEVICE_WORKSPACE_STATE
+    ref = paged_decode_reference(inp.q.cpu(), inp.k_cache.cpu(), inp.v_cache.cpu(),
+                                 inp.block_table.cpu(), inp.seq_lens.cpu(), inp.scale,
+                                 causal=True)
+    assert_close_to_oracle(out.cpu(), ref, "multi-token claim mask left set")
+    assert ws[256].item() == 0xFF
+    ws[256] = 0
+    again = paged_gqa_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_table, inp.seq_lens,
+                             inp.scale, causal=True, workspace=ws)
+    torch.cuda.synchronize()
+    assert read_device_status(ws) == 0
+    assert torch.equal(again, out)
+    assert not ws[256:256 + 128 * 256].any().item()
+
+
 def test_run_kernel_bounds_page_ids_by_num_blocks():
     """run_kernel takes num_blocks as the pool size (task.md:57-58): an id in a valid slot at or
     past num_blocks is flagged and read as page 0.  The tensors hold 16 pages, more than the
