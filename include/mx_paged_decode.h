@@ -69,7 +69,7 @@ extern "C" {
 #define MX_SCHEDULE_SPLIT_GRID_PAIRED 2 /* the split grid over pairs of adjacent KV heads, two
                                       waves of each workgroup per head: automatic plans on bf16
                                       and fp8 caches, head_dim 128, an even num_kv_heads >= 8,
-                                      2 * seqlen_q * group <= 16, and splits of >= 1024 tokens    */
+                                      2 * seqlen_q * group <= 16, and splits of >= 896 tokens     */
 #define MX_SCHEDULE_BALANCED_PAIRED 3 /* the balanced schedule over pairs of adjacent KV heads,
                                       on the same shapes as MX_SCHEDULE_SPLIT_GRID_PAIRED, and
                                       on fp8 caches also with 4 or 6 KV heads when the pairs of

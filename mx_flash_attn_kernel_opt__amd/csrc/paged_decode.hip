@@ -2348,7 +2348,7 @@ int64_t align_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 //    kMinTokensPerSplit long and at most kMaxTokensPerSplit.
 constexpr int64_t kMinTokensPerSplit = 128;   // amortises Q load, pipeline fill and partials
 constexpr int64_t kMaxTokensPerSplit = 16384;  // bounds one workgroup's share of a sequence
-constexpr int64_t kPairMinTokensPerSplit = 1024;  // paired split grid: shortest paired split
+constexpr int64_t kPairMinTokensPerSplit = 896;  // paired split grid: shortest paired split
 constexpr int64_t kMaxGridDim = 65535;
 // Query heads per KV head (MQA included).  Rows of one KV head are processed in 16- or 32-row
 // groups whatever the group size, so the limit only bounds how often K/V is re-streamed.
@@ -2601,7 +2601,9 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
   // 267-332 us apart, paired 290-303 us.  Interleaved A/B against one head per workgroup: long
   // B=4 128K 329.7 against 349.1 us, B=1 128K 91.5 against 94.5, B=4 32K 90.5 against 92.5.
   // Shorter splits lose: B=1 at 32K (512 tokens per paired split) 31.1 against 30.0 us, where
-  // the tree's partials of 16 rows lengthen the merge tail.
+  // the tree's partials of 16 rows lengthen the merge tail (with XCD-stable positions: 29.1
+  // against 27.8 us); at 928 tokens (contest case 13, B=1, 58 976 tokens) pairs win, 43.2
+  // against 44.3 us.
   if (pair_heads(pair_ok != kPairNone, num_splits, head_dim, num_kv_heads, rows)) {
     int64_t ns2 = auto_splits(batch * (num_kv_heads / 2), num_cus * groups_per_cu(head_dim), cap);
     if (ns2 > cap_pages) ns2 = cap_pages;

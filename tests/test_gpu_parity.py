@@ -756,7 +756,7 @@ def test_paired_random_shapes(seed):
     sq = r.choice([1, 1, 2]) if G <= 4 else 1
     P = r.choice([16, 32, 64])
     B = r.choice([r.randint(3, 6), r.randint(8, 48)])
-    # few sequences: long enough for paired splits of >= 1 024 tokens
+    # few sequences: long enough for paired splits of >= 896 tokens
     cap = r.choice([4096, 8192]) if B > 6 else r.choice([24576, 32768])
     special = [0, 1, P - 1, P, P + 1, cap]
     lens = [r.choice(special) if r.random() < 0.3 else r.randint(0, cap) for _ in range(B)]
