@@ -73,7 +73,9 @@ extern "C" {
 #define MX_SCHEDULE_BALANCED_PAIRED 3 /* the balanced schedule over pairs of adjacent KV heads,
                                       on the same shapes as MX_SCHEDULE_SPLIT_GRID_PAIRED, and
                                       on fp8 caches also with 4 or 6 KV heads when the pairs of
-                                      the batch are at least the workgroups                     */
+                                      the batch are at least the workgroups; on bf16 caches of
+                                      4 KV heads, pairs of heads 0 and 3, 1 and 2 when the
+                                      pairs of the batch outnumber the workgroups               */
 
 /* Phase flags for mx_paged_gqa_decode (0 = run everything). */
 #define MX_PHASE_MAIN_ONLY 1        /* split grid: run only the split-KV kernel, partials stay in

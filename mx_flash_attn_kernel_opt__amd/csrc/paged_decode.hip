@@ -579,6 +579,11 @@ struct MainShape {
   // query in dims 0..63 of the operand and zeros above, rows of the second in dims 64..127, so
   // each row's scores use its own head's keys; of its PV output each row keeps its own half.
   int pair_group;
+  // Mirrored pairs (MX_SCHEDULE_BALANCED_PAIRED on a bf16 cache of four KV heads, 1 KB token
+  // rows): kernel head p is the stored heads p and 3 - p (byte offsets 0 and 768, or 256 and
+  // 512, of the token row) instead of 2p and 2p + 1.  Its first G rows are head p's query rows,
+  // the next G head 3 - p's (row_offset, stored_head).
+  int pair_mirror;
   int seqlen_q;          // query tokens per sequence
   int causal;            // row t sees keys [0, L - seqlen_q + t + 1) (bottom-right aligned)
   int rows;              // seqlen_q * group
@@ -656,8 +661,8 @@ __device__ __forceinline__ int clamped_len_of(int L, const MainShape& sh, uint32
 }
 
 // Rows of q / out.  Row r = t*G + h of KV head kv of sequence b is q row
-// (b*seqlen_q + t)*num_heads + kv*G + h = row_base(b, kv) + row_offset(r): a wave-uniform base
-// plus a per-lane offset that is r itself for a single query token.
+// (b*seqlen_q + t)*num_heads + kv*G + h = row_base(b, kv) + row_offset(kv, r): a wave-uniform
+// base plus a per-lane offset that is r itself for a single query token.
 __device__ __forceinline__ int64_t row_base(int b, int kv, const MainShape& sh) {
   return (int64_t)b * sh.seqlen_q * sh.num_heads + kv * sh.group;
 }
@@ -665,8 +670,22 @@ __device__ __forceinline__ int64_t row_base(int b, int kv, const MainShape& sh) 
 __device__ __forceinline__ int row_token(int r, const MainShape& sh) {
   return sh.group_magic ? (int)__umulhi((uint32_t)r, sh.group_magic) : r;
 }
-__device__ __forceinline__ int row_offset(int r, const MainShape& sh) {
-  return r + row_token(r, sh) * (sh.num_heads - sh.group);
+// Stored KV head of half s (rows s*G .. s*G + G - 1 of each token, waves 2s and 2s + 1) of the
+// paired kernel head kv.
+__device__ __forceinline__ int stored_head(int kv, int s, const MainShape& sh) {
+  return sh.pair_mirror ? (s ? 3 - kv : kv) : 2 * kv + s;
+}
+__device__ __forceinline__ int row_offset(int kv, int r, const MainShape& sh) {
+  const int t = row_token(r, sh);
+  int off = r + t * (sh.num_heads - sh.group);
+  if (sh.pair_mirror) {
+    // Half s of kernel head kv is stored head h = stored_head(kv, s), whose query rows sit
+    // (h - 2kv - s) heads' rows away from those of half s of an adjacent pair.
+    const int g = sh.group >> 1;
+    const int s = r - t * sh.group >= g;
+    off += (stored_head(kv, s, sh) - 2 * kv - s) * g;
+  }
+  return off;
 }
 
 // Keys row r of a sequence of length seq sees: [0, limit).
@@ -687,7 +706,8 @@ __device__ __forceinline__ void load_q(bf16x8 (&qop)[D / 32], const uint16_t* q,
     if (sh.pair_group > 0) {  // q rows of 64 dims, placed in the row's half (MainShape)
       const int rr = live ? r : 0;
       const bool hi = rr - row_token(rr, sh) * sh.group >= sh.pair_group;
-      const uint16_t* qp = q + (row_base(b, kv, sh) + row_offset(rr, sh)) * (D / 2) + 8 * g4;
+      const uint16_t* qp =
+          q + (row_base(b, kv, sh) + row_offset(kv, rr, sh)) * (D / 2) + 8 * g4;
 #pragma unroll
       for (int i = 0; i < D / 32; ++i) {
         u32x4 x = {0, 0, 0, 0};
@@ -698,7 +718,7 @@ __device__ __forceinline__ void load_q(bf16x8 (&qop)[D / 32], const uint16_t* q,
       return;
     }
   }
-  const uint16_t* qp = q + (row_base(b, kv, sh) + (live ? row_offset(r, sh) : 0)) * D + 8 * g4;
+  const uint16_t* qp = q + (row_base(b, kv, sh) + row_offset(kv, live ? r : 0, sh)) * D + 8 * g4;
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) {
     u32x4 x = {0, 0, 0, 0};
@@ -1562,9 +1582,12 @@ struct SplitTree {
   uint32_t* counters;
   uint16_t* out;
   int64_t rbase;  // row_base of the unit
+  int kv;         // kernel KV head of the unit
   int r0;         // first row of the unit's row group
   int unit;       // (sequence, KV head and row group) index
-  __device__ __forceinline__ int64_t row(int hh) const { return rbase + row_offset(r0 + hh, sh); }
+  __device__ __forceinline__ int64_t row(int hh) const {
+    return rbase + row_offset(kv, r0 + hh, sh);
+  }
   __device__ __forceinline__ float* o(int hh, int slot) const {
     return part_o + (row(hh) * sh.num_splits + slot) * D;
   }
@@ -1660,7 +1683,7 @@ void mx_paged_decode_splitkv(
     // Empty sequence: defined as a zero output.
     if (split == 0)
       for (int e = tid; e < nrows * (D / 4); e += 64 * NW)
-        store_row4<D>(out, sh, row_base(b, kv, sh) + row_offset(r0 + e / (D / 4), sh),
+        store_row4<D>(out, sh, row_base(b, kv, sh) + row_offset(kv, r0 + e / (D / 4), sh),
                       4 * (e % (D / 4)), f32x4{0.f, 0.f, 0.f, 0.f}, -INFINITY);
     return;
   }
@@ -1697,8 +1720,8 @@ void mx_paged_decode_splitkv(
     // more chunk after its cache chunks in the waves' round-robin order.
     // Paired waves: each head's two waves take the new keys of their own head.
     const bool last = c_hi * kChunk >= seq;
-    const int hk = kPairW ? 2 * kv + (wv >> 1) : kv;       // the stored head this wave streams
-    const int wk = kPairW ? (wv & 1) : wv;                  // its place among the head's waves
+    const int hk = kPairW ? stored_head(kv, wv >> 1, sh) : kv;  // stored head of this wave
+    const int wk = kPairW ? (wv & 1) : wv;  // its place among the head's waves
     constexpr int kHeadWaves = kPairW ? 2 : NW;
     const NewTokens<kFp8> nt{sh, b, hk, ext.cache, last && wk == (c_end - c_lo) % kHeadWaves,
                        grp == 0,    ext.at,     bt_row, status};
@@ -1708,8 +1731,8 @@ void mx_paged_decode_splitkv(
   } else if constexpr (kPairW) {
     static_assert(NW == 4 && KT == 1, "paired waves: four waves, one row tile");
     stream_chunks<D, NBUF, 2, kCausal, KT, NoExtraChunk, kFp8>(
-        st, qop, kc, vc, bt_row, 2 * kv + (wv >> 1), c_lo, c_end, ext.cache, c_mask, row_lim,
-        wv & 1, L::ktile(lds, wv), sh, bad_page);
+        st, qop, kc, vc, bt_row, stored_head(kv, wv >> 1, sh), c_lo, c_end, ext.cache, c_mask,
+        row_lim, wv & 1, L::ktile(lds, wv), sh, bad_page);
   } else {
     stream_chunks<D, NBUF, NW, kCausal, KT, NoExtraChunk, kFp8>(
         st, qop, kc, vc, bt_row, kv, c_lo, c_end, ext.cache, c_mask, row_lim, wv,
@@ -1728,7 +1751,7 @@ void mx_paged_decode_splitkv(
       o = merged_head_pair<D>(lds, hh, d, lse, sh);
     else
       o = merged_head<D, NW, KT>(lds, hh, d, lse);
-    const int64_t row = row_base(b, kv, sh) + row_offset(r0 + hh, sh);
+    const int64_t row = row_base(b, kv, sh) + row_offset(kv, r0 + hh, sh);
     if (single) {
       store_row4<D>(out, sh, row, d, o, lse);
     } else if (sh.fused_combine) {  // read back by another workgroup of this launch
@@ -1746,7 +1769,7 @@ void mx_paged_decode_splitkv(
 
   // This split's partial is level-0 item `split` of the unit's merge tree.
   const int nsv = (seq + sh.tokens_per_split - 1) / sh.tokens_per_split;  // splits with tokens
-  const SplitTree<D> tree{sh,  part_o, part_lse, counters, out, row_base(b, kv, sh), r0,
+  const SplitTree<D> tree{sh,  part_o, part_lse, counters, out, row_base(b, kv, sh), kv, r0,
                           b * (int)gridDim.x + bx};
   // Up to 32 splits merge in one level: the last arrival loads every partial in one round trip
   // (long B=1 32K, 32 splits: 27.36-27.41 against 27.53-27.55 us; long B=4 32K, 16 paired
@@ -1774,6 +1797,7 @@ struct BalancedTree {
   uint32_t* counters;
   uint16_t* out;
   int64_t rbase;  // row_base of the unit
+  int kv;         // kernel KV head of the unit
   int r0;         // first row of the unit's row group
   int slot0;
   int tile_rows;
@@ -1787,7 +1811,7 @@ struct BalancedTree {
     return counters + (int64_t)level * kMaxSlots + slot0 + slot;
   }
   __device__ __forceinline__ void store(int hh, int d, f32x4 v, float l) const {
-    store_row4<D>(out, sh, rbase + row_offset(r0 + hh, sh), d, v, l);
+    store_row4<D>(out, sh, rbase + row_offset(kv, r0 + hh, sh), d, v, l);
   }
 };
 
@@ -2009,8 +2033,8 @@ void mx_paged_decode_balanced(
         // Fused append: the piece holding the unit's last schedule chunk also takes the new
         // keys, as one more chunk after its cache chunks in the waves' round-robin order.
         // Paired waves: each head's two waves take the new keys of their own head.
-        const int hk = kPairW ? 2 * kv + (wv >> 1) : kv;   // the stored head this wave streams
-        const int wk = kPairW ? (wv & 1) : wv;              // its place among the head's waves
+        const int hk = kPairW ? stored_head(kv, wv >> 1, sh) : kv;  // stored head of this wave
+        const int wk = kPairW ? (wv & 1) : wv;  // its place among the head's waves
         constexpr int kHeadWaves = kPairW ? 2 : NW;
         const NewTokens<kFp8> nt{sh, b, hk, ext.cache, cb == n_b && wk == (c_end - ca) % kHeadWaves,
                            grp == 0, ext.at, bt_row, status};
@@ -2020,8 +2044,8 @@ void mx_paged_decode_balanced(
       } else if constexpr (kPairW) {
         static_assert(NW == 4 && KT == 1, "paired waves: four waves, one row tile");
         stream_chunks<D, NBUF, 2, kCausal, KT, NoExtraChunk, kFp8>(
-            st, qop, kc, vc, bt_row, 2 * kv + (wv >> 1), ca, c_end, ext.cache, c_mask, row_lim,
-            wv & 1, L::ktile(lds, wv), sh, bad_page);
+            st, qop, kc, vc, bt_row, stored_head(kv, wv >> 1, sh), ca, c_end, ext.cache, c_mask,
+            row_lim, wv & 1, L::ktile(lds, wv), sh, bad_page);
       } else {
         stream_chunks<D, NBUF, NW, kCausal, KT, NoExtraChunk, kFp8>(
             st, qop, kc, vc, bt_row, kv, ca, c_end, ext.cache, c_mask, row_lim, wv,
@@ -2041,7 +2065,7 @@ void mx_paged_decode_balanced(
             o = merged_head_pair<D>(lds, hh, d, lse, sh);
           else
             o = merged_head<D, NW, KT>(lds, hh, d, lse);
-          store_row4<D>(out, sh, rbase + row_offset(r0 + hh, sh), d, o, lse);
+          store_row4<D>(out, sh, rbase + row_offset(kv, r0 + hh, sh), d, o, lse);
         }
       } else {
         // Piece k of the unit goes to slot slot0 + k and is level-0 item k of its merge tree.
@@ -2063,7 +2087,7 @@ void mx_paged_decode_balanced(
             if (d == 0) store_partial1(pl + hh, lse);
           }
         }
-        const BalancedTree<D> tree{sh, part_o, part_lse, counters, out, rbase, r0, slot0, TR};
+        const BalancedTree<D> tree{sh, part_o, part_lse, counters, out, rbase, kv, r0, slot0, TR};
         merge_tree<D, NW, kMergeFanIn>(tree, item, npieces, nrows, s_lse, &s_int[NW + 2]);
       }
       // The merged states in LDS share bytes with the K tiles the next piece streams into:
@@ -2391,6 +2415,12 @@ bool split_tree_fits(int64_t units, int64_t splits, int64_t o_bytes) {
 // configurations unchanged.
 constexpr int kChunkPositions = 8;
 constexpr int kUnitOverhead = 8 * kChunkPositions;
+// Mirrored pairs (MainShape::pair_mirror) are charged 80 positions per pair unit (the weight of
+// 10 single-head chunks, 5 of their own).  Interleaved A/B on config 4: 64, 80, 96, 112 and 128
+// positions 75.9-76.1, 74.7-74.8, 74.8-74.9, 74.9-75.0 and 75.1-75.2 us (single heads
+// 75.6-75.9); config 4's lengths at page size 16: 80 positions 75.4, 96 75.9, 128 75.9 against
+// 77.1 us single-head.
+constexpr int kMirroredPairOverhead = 10 * kChunkPositions;
 static_assert((kChunkPositions & (kChunkPositions - 1)) == 0,
               "the balanced kernels divide by the chunk weight with a shift");
 // Balanced schedule limits: the largest batch whose seq_lens scan stays within two passes of
@@ -2416,6 +2446,7 @@ struct Plan {
   int64_t o_offset = 0;
   int64_t workspace_bytes = kStatusBytes;
   int chunk_shift = 0;
+  bool pair_mirror = false;       // MX_SCHEDULE_BALANCED_PAIRED: mirrored pairs (MainShape)
 };
 
 // KV heads of the kernels' units: pairs of the (kernel) heads on the paired schedules.
@@ -2457,12 +2488,32 @@ int query_num_cus(int64_t* num_cus) {
 // pair_ok values (pair_ok_for): no pairs; bf16 rules; fp8 rules, where 4 KV heads (512-byte
 // token rows) also pair on the balanced schedule when there are at least as many pair units as
 // workgroups (a ragged batch: config 4's lengths on an fp8 cache, 63.7-63.9 against 67.5-68.5
-// us; with fewer units, e.g. contest cases 8 and 11 on fp8, pairs lost 16 and 8 %).
+// us; with fewer units, e.g. contest cases 8 and 11 on fp8, pairs lost 16 and 8 %).  bf16
+// caches of 4 KV heads (1 KB token rows) pair on the balanced schedule as mirrored pairs
+// (MainShape::pair_mirror) when there are more pair units than workgroups (mirrored_pairs).
 constexpr int kPairNone = 0, kPairBf16 = 1, kPairFp8 = 2;
 bool pair_heads(bool pair_ok, int64_t num_splits, int64_t head_dim, int64_t num_kv_heads,
                 int64_t rows) {
   return pair_ok && num_splits == 0 && head_dim == 128 && num_kv_heads % 2 == 0 &&
          num_kv_heads * head_dim * 2 >= 2048 && 2 * rows <= 16;
+}
+
+// Mirrored pairs (MainShape::pair_mirror): balanced pairs of heads 0 and 3, 1 and 2 of a bf16
+// cache with 4 KV heads at head_dim 128, when the batch has more pair units than workgroups.
+// Interleaved A/B against single heads (B ragged or uniform lengths, Hq=28, page size 64 unless
+// noted):
+// - config 4 (B=256, lengths up to 8 192): 74.7-74.8 against 75.9-76.2 us, graph replays 74.9
+//   against 76.6; the same lengths at page size 16: 75.4 against 77.1; ragged B=192: 55.7
+//   against 57.2; ragged B=512 up to 4 096: 84.6 against 85.3;
+// - uniform B=256 at 2 048 tokens: 163.3 against 163.3; B=192 at 4 096: 243.5 against 242.4.
+// Adjacent pairs (0 and 1, 2 and 3) lost on config 4 (77.6-78.0 us), pairs 0 and 2, 1 and 3
+// lost less (76.7-77.0), both at the 8 positions per unit of 2 KB pairs, where mirrored pairs
+// took 75.6-75.7.  With as many pair units as workgroups (B=128) pairs lost: ragged 42.3
+// against 41.9, uniform at 4 096 tokens 162.2 against 157.8 us.
+bool mirrored_pairs(int pair_ok, int64_t num_splits, int64_t head_dim, int64_t num_kv_heads,
+                    int64_t rows, int64_t units, int64_t groups) {
+  return pair_ok == kPairBf16 && num_kv_heads == 4 &&
+         pair_heads(true, num_splits, head_dim, 2 * num_kv_heads, rows) && units / 2 > groups;
 }
 
 // Automatic split count of the split grid: enough splits for `slots` resident workgroups over
@@ -2585,9 +2636,12 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
     const bool narrow_pairs =
         pair_ok == kPairFp8 && num_kv_heads >= 4 && num_kv_heads % 2 == 0 &&
         pair_heads(true, num_splits, head_dim, 2 * num_kv_heads, rows) && units / 2 >= groups;
+    const bool mirrored =
+        mirrored_pairs(pair_ok, num_splits, head_dim, num_kv_heads, rows, units, groups);
     if (pair_heads(pair_ok != kPairNone, num_splits, head_dim, num_kv_heads, rows) ||
-        narrow_pairs) {
+        narrow_pairs || mirrored) {
       plan->schedule = MX_SCHEDULE_BALANCED_PAIRED;
+      plan->pair_mirror = mirrored;
       plan->rows = 2 * rows;
       line_units = units / 2;
       slot_rows = 2 * rows;
@@ -2813,7 +2867,8 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   sh.num_groups = (int)plan.groups;
   // A paired unit's chunk holds two heads' rows: twice a single head's weight on the line.
   sh.chunk_weight = paired ? 2 * kChunkPositions : kChunkPositions;
-  sh.unit_overhead = kUnitOverhead;
+  sh.unit_overhead = plan.pair_mirror ? kMirroredPairOverhead : kUnitOverhead;
+  sh.pair_mirror = plan.pair_mirror ? 1 : 0;
   sh.num_slots = (int)plan.slots;
   sh.o_out = o_out;
   sh.lse_out = lse_out;

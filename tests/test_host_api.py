@@ -194,13 +194,16 @@ def test_split_grid_plan_invariants(B, Hq, Hkv, D, P, max_pages, cap, ns_req):
     (128, 32, 4, 64, 0, 512, False),     # two 2-wave workgroups per CU at D=64
     (64, 16, 2, 256, 0, 256, False),     # one per CU at D=256
     (4, 32, 8, 128, -7, 7, False),       # forced workgroup count: never paired
-    (512, 28, 4, 128, 0, 256, False),    # 4 KV heads: 1 KB token rows are not paired
+    (512, 28, 4, 128, 0, 256, True),     # 4 KV heads: mirrored pairs, more pairs than groups
+    (128, 28, 4, 128, 0, 256, False),    # 4 KV heads, as many pairs as groups: single heads
+    (192, 28, 2, 128, 0, 256, False),    # 2 KV heads (512-byte token rows): single heads
     (3, 32, 8, 128, -9000, 4095, False),  # clamped to the 8^4 merge tree
     (32, 128, 16, 128, 0, 256, True),    # 16 KV heads, group 8: pairs of 16 rows
 ])
 def test_balanced_plan(B, Hq, Hkv, D, ns_req, groups, paired):
     """Slots of the balanced schedule: one per workgroup and one per unit, of min(rows, 16)
-    rows; paired units are two adjacent KV heads with both heads' rows."""
+    rows; paired units are two KV heads (adjacent, or heads 0 and 3, 1 and 2 of four) with both
+    heads' rows."""
     p = plan(B, Hq, Hkv, D, 16, 256, 0, ns_req, num_cus=256)
     assert p["schedule"] == ("balanced_paired" if paired else "balanced")
     assert p["workgroups"] == groups and p["splits"] == 0
@@ -219,7 +222,7 @@ def test_policy_on_the_north_star_configs():
         "tiny": ("split_grid", 4), "llama3_8b": ("balanced_paired", 256),
         "long_b1_32k": ("split_grid", 32), "long_b1_128k": ("split_grid_paired", 64),
         "long_b4_32k": ("split_grid_paired", 16), "long_b4_128k": ("split_grid_paired", 16),
-        "ragged": ("balanced", 256), "sweep_b32_16k": ("balanced_paired", 256),
+        "ragged": ("balanced_paired", 256), "sweep_b32_16k": ("balanced_paired", 256),
         "sweep_b128_16k": ("balanced_paired", 256), "sweep_d64": ("balanced", 512),
         "sweep_d256": ("balanced", 256),
     }
