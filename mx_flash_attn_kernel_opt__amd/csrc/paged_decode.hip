@@ -2421,6 +2421,18 @@ constexpr int kUnitOverhead = 8 * kChunkPositions;
 // 75.6-75.9); config 4's lengths at page size 16: 80 positions 75.4, 96 75.9, 128 75.9 against
 // 77.1 us single-head.
 constexpr int kMirroredPairOverhead = 10 * kChunkPositions;
+// fp8 caches: a chunk moves half a bf16 chunk's bytes in about half the time, while a unit's
+// query load, pipeline fill and merge take as long, so a unit costs more chunk positions: 160
+// (192 for the pairs of 512- and 768-byte token rows).  Interleaved A/B on ragged lengths
+// (config 4's recipe, B=256, up to 8 192 tokens), charges 64 / 128 / 160 / 192 / 256 / 320:
+// - 4 KV heads, fp8 pairs (config 4): 61.6 / 48.0 / 45.5 / 44.3 / 44.4 / 45.6 us;
+// - 8 KV heads, pairs, page size 16: 103.1 / 78.6 / 78.5 / 79.5 / 81.1 / 82.9; page size 64:
+//   101.7 / 77.8 / 77.9 / 79.0 / 79.8 / 82.4;
+// - 2 KV heads, single heads: head_dim 128 35.7 / 27.9 / 27.0 / 27.5 / 28.4 / 29.7, head_dim
+//   256 (B=128) 32.9 / 29.6 / 28.7 / 28.4 / 29.9 / 30.7.
+constexpr int kFp8UnitOverhead = 20 * kChunkPositions;
+constexpr int kFp8NarrowPairOverhead = 24 * kChunkPositions;
+constexpr int kMaxUnitOverhead = kFp8NarrowPairOverhead;  // of every charge above
 static_assert((kChunkPositions & (kChunkPositions - 1)) == 0,
               "the balanced kernels divide by the chunk weight with a shift");
 // Balanced schedule limits: the largest batch whose seq_lens scan stays within two passes of
@@ -2601,7 +2613,7 @@ int make_plan(int64_t batch, int64_t seqlen_q, int64_t num_heads, int64_t num_kv
   plan->chunk_shift = shift;
   const int64_t units = batch * num_kv_heads * row_tiles;
   const bool balanced_ok = batch <= kBalancedMaxBatch && units <= kBalancedMaxUnits &&
-                           units * (ceil_div(cap, kChunk) * kChunkPositions + kUnitOverhead) <
+                           units * (ceil_div(cap, kChunk) * kChunkPositions + kMaxUnitOverhead) <
                                kBalancedMaxLine;
   // Short capacities favour one split per unit (no length scan, no merge): the balanced
   // schedule pays off from 2 048 tokens, or from 1 024 with at least 512 units.
@@ -2867,7 +2879,9 @@ hipError_t launch(const Plan& plan, const void* q, const void* k, const void* v,
   sh.num_groups = (int)plan.groups;
   // A paired unit's chunk holds two heads' rows: twice a single head's weight on the line.
   sh.chunk_weight = paired ? 2 * kChunkPositions : kChunkPositions;
-  sh.unit_overhead = plan.pair_mirror ? kMirroredPairOverhead : kUnitOverhead;
+  sh.unit_overhead = !kv.fp8          ? (plan.pair_mirror ? kMirroredPairOverhead : kUnitOverhead)
+                     : paired && num_kv_heads * D < 1024 ? kFp8NarrowPairOverhead
+                                                         : kFp8UnitOverhead;
   sh.pair_mirror = plan.pair_mirror ? 1 : 0;
   sh.num_slots = (int)plan.slots;
   sh.o_out = o_out;
