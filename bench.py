@@ -6,9 +6,12 @@
 One step = one decode-attention call over the whole batch of the workload (default: the
 Llama-3-8B decode shape the metric is quoted on, B=64 Hq=32 Hkv=8 D=128 P=16 L=4096), inputs
 resident in HBM.  The timed region is K back-to-back steps on one stream, bracketed by
-torch.cuda.synchronize(); inside it HIP events bracket the main kernel of every step (the
-balanced single launch, or the split-KV kernel of the split grid, whose combine kernel runs
-after the second event).  Prints ONE JSON line:
+torch.cuda.synchronize(), after W untimed warmup steps; before those, the same calls run
+untimed for --settle-ms (default 40 ms, recorded in the line as "settle"), past the slow
+stretch of a fresh process's first ~15 ms of GPU load (see settle_device).  A second pass
+brackets the main kernel of every step with HIP events (the balanced single launch, or the
+split-KV kernel of the split grid, whose combine kernel runs after the second event).  Prints
+ONE JSON line:
   value      effective KV GB/s of whole steps = algorithmic K+V bytes / (ms_per_step)
   roofline   achieved GB/s of the main kernel alone (events around it) against 8 TB/s
   cpu_baseline  the fp32 oracle (oracle/paged_attention.py) timed on this host on a bounded
@@ -80,9 +83,32 @@ def _traffic_from_profile(kernel: str, workload: str):
     return None
 
 
+def settle_device(call_once, settle_ms: float) -> int:
+    """Issue untimed calls until `settle_ms` of wall time has passed (synchronised every 64
+    calls); returns the number of calls.  A fresh process's first ~10 ms of back-to-back calls
+    include a slow stretch: per-10-call event times of ragged decode read ~74.5 us for calls
+    1-30, 76-79 us for calls 40-130 and 74.0 +- 0.5 us from then on (Llama-3-8B decode: 159-160
+    against 157 us), so a timed region that starts inside the first ~15 ms measures that
+    transient instead of the steady state of a decode loop."""
+    if settle_ms <= 0:
+        return 0
+    n = 0
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < settle_ms:
+        for _ in range(64):
+            call_once(n)
+            n += 1
+        torch.cuda.synchronize()
+    return n
+
+
+SETTLE_MS = 40.0
+
+
 def time_workload(inp: W.DecodeInputs, steps: int, warmup: int, num_splits: int = 0,
-                  graph: bool = False) -> dict:
+                  graph: bool = False, settle_ms: float = SETTLE_MS) -> dict:
     """Time `steps` calls after `warmup`; events bracket the split-KV kernel of each step.
+    Before the warmup, settle_device runs the same calls untimed for `settle_ms`.
     With `graph`, also time the same calls captured in a HIP graph and replayed."""
     spec = inp.spec
     stream = torch.cuda.current_stream()
@@ -136,6 +162,7 @@ def time_workload(inp: W.DecodeInputs, steps: int, warmup: int, num_splits: int 
         kern = [a.elapsed_time(b) * 1e3 for a, b in ev] if kernel_events else None
         return start.elapsed_time(end) / steps, kern, wall
 
+    settle_calls = settle_device(lambda i: step(calls[i % len(calls)]), settle_ms)
     for i in range(warmup):
         step(calls[i % len(calls)])
     # The timed region: `steps` calls back to back.
@@ -162,6 +189,7 @@ def time_workload(inp: W.DecodeInputs, steps: int, warmup: int, num_splits: int 
     kern_mean = statistics.fmean(kern_us)
     return {
         "kernel_us_events_mean": statistics.fmean(kern_ev_us),
+        "settle": {"ms": settle_ms, "calls": settle_calls},
         "kernel_us_events_median": statistics.median(kern_ev_us),
         "nbytes": nbytes,
         "fp8": fp8,
@@ -587,6 +615,7 @@ def result_line(args, spec, r, cpu=None) -> dict:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": r["settle"],
         "ms_per_step": round(r["ms_per_step"], 5),
         "us_per_call": round(r["ms_per_step"] * 1e3, 2),
         "hbm_frac": round(r["value_gbps"] / HBM_PEAK_GBPS, 4),
@@ -648,6 +677,9 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                    help="untimed calls for this many ms before the warmup steps, past the "
+                         "start-of-load transient of a fresh process (0: none)")
     ap.add_argument("--workload", default=W.BENCH_DEFAULT)
     ap.add_argument("--num-splits", type=int, default=0)
     ap.add_argument("--seed", type=int, default=0)
@@ -729,7 +761,8 @@ def main(argv=None) -> int:
         inp.k_cache = inp.k_cache.to(torch.float8_e4m3fn)
         inp.v_cache = inp.v_cache.to(torch.float8_e4m3fn)
         torch.cuda.empty_cache()
-    r = time_workload(inp, args.steps, args.warmup, args.num_splits, graph=args.graph)
+    r = time_workload(inp, args.steps, args.warmup, args.num_splits, graph=args.graph,
+                      settle_ms=args.settle_ms)
     cpu = None if args.no_cpu_baseline else cpu_baseline(inp, args.cpu_budget)
     line = result_line(args, spec, r, cpu)
     if args.shards > 0:
@@ -758,7 +791,8 @@ def main(argv=None) -> int:
             steps = max(10, min(args.steps, int(2e11 // max(nbytes, 1))))
             cmd = [sys.executable, os.path.abspath(__file__), "--workload", name, "--steps",
                    str(steps), "--warmup", str(min(args.warmup, steps)), "--seed",
-                   str(args.seed), "--no-cpu-baseline"] + (["--graph"] if args.graph else [])
+                   str(args.seed), "--no-cpu-baseline", "--settle-ms", str(args.settle_ms)] + (
+                       ["--graph"] if args.graph else [])
             child = subprocess.run(cmd, capture_output=True, text=True)
             lines = [ln for ln in child.stdout.splitlines() if ln.startswith("{")]
             if child.returncode != 0 or not lines:
@@ -768,7 +802,8 @@ def main(argv=None) -> int:
         for name in (W.BENCH_DEFAULT, "sweep_d64"):
             cmd = [sys.executable, os.path.abspath(__file__), "--workload", name, "--kv-dtype",
                    "fp8", "--steps", str(args.steps), "--warmup", str(args.warmup), "--seed",
-                   str(args.seed), "--no-cpu-baseline"] + (["--graph"] if args.graph else [])
+                   str(args.seed), "--no-cpu-baseline", "--settle-ms", str(args.settle_ms)] + (
+                       ["--graph"] if args.graph else [])
             child = subprocess.run(cmd, capture_output=True, text=True)
             lines = [ln for ln in child.stdout.splitlines() if ln.startswith("{")]
             if child.returncode != 0 or not lines:

@@ -1454,17 +1454,24 @@ __device__ __forceinline__ void merge_elems(const Tree& tree, int e0, int total,
   float ls[E][W];
   f32x4 vs[E][W];
   int hh[E], d[E];
+  // Item t of the group sits t * stride slots after the first: the row's addresses are formed
+  // once and stepped by a uniform stride (forming each item's address from its slot instead took
+  // a dozen dependent integer instructions per load).
+  const int lse_step = tree.lse_step() * stride;
+  const int o_step = tree.o_step() * stride;
 #pragma unroll
   for (int q = 0; q < E; ++q) {
     const int e = e0 + q * 64 * NW;
     const int ee = e < total ? e : e0;
     hh[q] = ee / (D / 4);
     d[q] = 4 * (ee - hh[q] * (D / 4));
+    const float* lp = tree.lse(hh[q], gslot);
+    const float* op = tree.o(hh[q], gslot) + d[q];
 #pragma unroll
     for (int t = 0; t < W; ++t) {
-      const int sl = gslot + (t < gsize ? t : 0) * stride;
-      ls[q][t] = load_partial1(tree.lse(hh[q], sl));
-      vs[q][t] = load_partial4(tree.part_o, tree.o(hh[q], sl) + d[q]);
+      const int tt = t < gsize ? t : 0;
+      ls[q][t] = load_partial1(lp + tt * lse_step);
+      vs[q][t] = load_partial4(tree.part_o, op + tt * o_step);
     }
   }
 #pragma unroll
@@ -1529,7 +1536,8 @@ __device__ __forceinline__ void merge_group(const Tree& tree, int gslot, int str
 // written.
 //
 // `tree` provides o(hh, slot) / lse(hh, slot) (the fp32 partial row hh of a level-0 slot and its
-// log2-sum-exp), counter(level, slot) (the arrival counter of the level's group whose first item
+// log2-sum-exp), o_step() / lse_step() (the floats between those of consecutive slots of a row),
+// counter(level, slot) (the arrival counter of the level's group whose first item
 // is at `slot`) and store(hh, d, o, lse) (the final store of dims d..d+3 of row hh).  s_lse holds
 // nrows floats.
 template <int D, int NW, int F, class Tree>
@@ -1598,6 +1606,9 @@ struct SplitTree {
     return counters + (int64_t)level * kMaxSlots + (int64_t)unit * sh.split_groups +
            slot / kMergeFanIn;
   }
+  // floats between the lse / o entries of consecutive slots of one row
+  __device__ __forceinline__ int lse_step() const { return 1; }
+  __device__ __forceinline__ int o_step() const { return D; }
   __device__ __forceinline__ void store(int hh, int d, f32x4 v, float l) const {
     store_row4<D>(out, sh, row(hh), d, v, l);
   }
@@ -1810,6 +1821,9 @@ struct BalancedTree {
   __device__ __forceinline__ uint32_t* counter(int level, int slot) const {
     return counters + (int64_t)level * kMaxSlots + slot0 + slot;
   }
+  // floats between the lse / o entries of consecutive slots of one row
+  __device__ __forceinline__ int lse_step() const { return tile_rows; }
+  __device__ __forceinline__ int o_step() const { return tile_rows * D; }
   __device__ __forceinline__ void store(int hh, int d, f32x4 v, float l) const {
     store_row4<D>(out, sh, rbase + row_offset(kv, r0 + hh, sh), d, v, l);
   }
