@@ -182,7 +182,7 @@ def time_workload(inp: W.DecodeInputs, steps: int, warmup: int, num_splits: int 
         warm = {"us_per_call": round(w_ms * 1e3, 2),
                 "kernel_us_mean": round(statistics.fmean(w_kern), 2),
                 "GBps": round(nbytes / (w_ms * 1e-3) / 1e9, 1)}
-    graphed = time_graph(inp, pools, out, ws, num_splits, steps) if graph else None
+    graphed = time_graph(inp, pools, out, ws, num_splits, steps, settle_ms) if graph else None
     flags = pkg.read_device_status(ws)
     if flags:
         raise RuntimeError(f"device status flags {flags} raised during the benchmark")
@@ -206,7 +206,8 @@ def time_workload(inp: W.DecodeInputs, steps: int, warmup: int, num_splits: int 
     }
 
 
-def time_graph(inp: W.DecodeInputs, pools, out, ws, num_splits: int, steps: int) -> dict:
+def time_graph(inp: W.DecodeInputs, pools, out, ws, num_splits: int, steps: int,
+               settle_ms: float = SETTLE_MS) -> dict:
     """The workload's calls captured in a HIP graph (one call per K/V pool, repeated up to 16
     calls) and replayed until about `steps` calls ran: the per-call time without host launch
     overhead.  The library allocates, clears and synchronises nothing inside a call that gets a
@@ -227,6 +228,8 @@ def time_graph(inp: W.DecodeInputs, pools, out, ws, num_splits: int, steps: int)
     torch.cuda.synchronize()
     replays = max(2, steps // per_graph)
     cur = torch.cuda.current_stream()
+    # Capturing left the GPU idle: settle again (replays, untimed) before the timed replays.
+    settle_device(lambda i: g.replay() if i % per_graph == 0 else None, settle_ms)
     g.replay()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(cur)
