@@ -197,21 +197,25 @@ def c500_spec(case: int, table: str = "arange") -> DecodeSpec:
                       table=table, description=f"contest case {case}: b{batch} cap{cap} kv{kv}")
 
 
-_SHAPE_NAME = re.compile(r"(uniform|ragged)_b(\d+)_hq(\d+)_hkv(\d+)_l(\d+)")
+_SHAPE_NAME = re.compile(r"(uniform|ragged)_b(\d+)_hq(\d+)_hkv(\d+)_l(\d+)(?:_d(\d+))?")
 
 
-def shape_spec(kind: str, batch: int, num_heads: int, num_kv_heads: int, length: int) -> DecodeSpec:
-    """Head_dim 128, page_size 16 decode of `batch` sequences: every one `length` keys
-    ("uniform"), or config 4's recipe up to `length` ("ragged": log-uniform in [1, length], 10 %
-    in [1, 15])."""
+def shape_spec(kind: str, batch: int, num_heads: int, num_kv_heads: int, length: int,
+               head_dim: int = 128) -> DecodeSpec:
+    """Page_size 16 decode of `batch` sequences (head_dim 128 unless a `_d<D>` suffix says
+    otherwise): every one `length` keys ("uniform"), or config 4's recipe up to `length`
+    ("ragged": log-uniform in [1, length], 10 % in [1, 15])."""
     pages = math.ceil(length / 16)
     name = f"{kind}_b{batch}_hq{num_heads}_hkv{num_kv_heads}_l{length}"
+    if head_dim != 128:
+        name += f"_d{head_dim}"
     if kind == "uniform":
-        return DecodeSpec(name, batch, num_heads, num_kv_heads, 128, 16, pages, "fixed", (length,),
-                          description=f"uniform B={batch} Hq={num_heads} Hkv={num_kv_heads} L={length}")
+        return DecodeSpec(name, batch, num_heads, num_kv_heads, head_dim, 16, pages, "fixed",
+                          (length,), description=f"uniform B={batch} Hq={num_heads} "
+                                                 f"Hkv={num_kv_heads} L={length} D={head_dim}")
     if kind == "ragged":
-        return DecodeSpec(name, batch, num_heads, num_kv_heads, 128, 16, pages, "loguniform_ragged",
-                          (1, length, 0.10, 15),
+        return DecodeSpec(name, batch, num_heads, num_kv_heads, head_dim, 16, pages,
+                          "loguniform_ragged", (1, length, 0.10, 15),
                           description=f"ragged B={batch} Hq={num_heads} Hkv={num_kv_heads} "
                                       f"L log-uniform [1,{length}], 10% in [1,15]")
     raise ValueError(f"unknown shape kind {kind!r}")
@@ -226,9 +230,10 @@ def get_spec(name: str) -> DecodeSpec:
         return c500_spec(int(name[len("c500_case"):]))
     m = _SHAPE_NAME.fullmatch(name)
     if m:
-        return shape_spec(m.group(1), *(int(x) for x in m.groups()[1:]))
+        return shape_spec(m.group(1), *(int(x) for x in m.groups()[1:5]),
+                          head_dim=int(m.group(6)) if m.group(6) else 128)
     raise KeyError(f"unknown workload {name!r}; known: {sorted(NORTH_STAR)}, c500_case1..14, "
-                   "uniform_bB_hqH_hkvK_lL and ragged_bB_hqH_hkvK_lL")
+                   "uniform_bB_hqH_hkvK_lL and ragged_bB_hqH_hkvK_lL (optional _dD suffix)")
 
 
 # ---------------------------------------------------------------------------------------
