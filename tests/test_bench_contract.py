@@ -36,3 +36,15 @@ def test_case_table_matches_the_reference_harness():
 def test_more_than_one_gpu_is_refused(argv, capsys):
     assert bench.main(argv) == 2
     assert "one GPU" in capsys.readouterr().err
+
+
+def test_settle_runs_calls_for_the_requested_time(monkeypatch):
+    """settle_device issues calls in synchronised batches of 64 until settle_ms has passed, and
+    none for settle_ms <= 0 (the host side only: the synchronisation is stubbed)."""
+    syncs = []
+    monkeypatch.setattr(bench.torch.cuda, "synchronize", lambda: syncs.append(1))
+    calls = []
+    assert bench.settle_device(calls.append, 0) == 0 and calls == [] and syncs == []
+    n = bench.settle_device(calls.append, 5.0)
+    assert n == len(calls) and n >= 64 and n % 64 == 0
+    assert calls == list(range(n)) and len(syncs) == n // 64
