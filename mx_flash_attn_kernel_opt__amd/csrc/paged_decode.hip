@@ -1378,7 +1378,14 @@ constexpr int kMaxMergeItems = 8 * 8 * 8 * 8;
 // from the arrival counter (arrive_last).  A plain-store variant with __threadfence() in every
 // thread was measured first: it writes back the L2 per wave, and config 2 with 1 024 workgroups
 // ran 505 us instead of 174.
+// The merging workgroup's loads (rows and log-sum-exps) also carry the nontemporal hint: a
+// partial is read once.  Interleaved A/B against sc1 loads without it, outputs bitwise equal:
+// ragged 72.2 against 74.1 us (graph replays 72.4 against 74.4, seed 3 68.1 against 70.2),
+// contest cases 11 and 8 42.5 against 43.1 and 19.3 against 19.6 us, long contexts 0.1-0.3 us
+// faster.  The same hint on the partial stores was slower (long B=1 32K 28.6 against 27.4 us,
+// ragged 75.0 against 74.3).
 constexpr int kCachePolicySc1 = 16;  // buffer intrinsics' aux bit for sc1
+constexpr int kCachePolicyNt = 2;    // buffer intrinsics' aux bit for nt
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(const float* base) {
   // Raw buffer over [base, base + 2^31 - 1): stride 0, dword 3 = 0x00020000 (32-bit data, no
   // swizzle), as for every gfx9 raw buffer.
@@ -1397,10 +1404,15 @@ __device__ __forceinline__ f32x4 load_partial4(const float* base, const float* p
   return __builtin_bit_cast(
       f32x4, __builtin_amdgcn_raw_buffer_load_b128(partial_rsrc(base),
                                                    (int)((const char*)p - (const char*)base), 0,
-                                                   kCachePolicySc1));
+                                                   kCachePolicySc1 | kCachePolicyNt));
 }
-__device__ __forceinline__ float load_partial1(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// A log-sum-exp stored by store_partial1, read through a resource based at the log-sum-exp region
+// (also below 2^31 bytes) with the same policy as load_partial4.
+__device__ __forceinline__ float load_partial1(const float* base, const float* p) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_raw_buffer_load_b32(partial_rsrc(base),
+                                                  (int)((const char*)p - (const char*)base), 0,
+                                                  kCachePolicySc1 | kCachePolicyNt));
 }
 
 // Arrival of this workgroup at `counter`, which `expected` workgroups reach once each; returns,
@@ -1470,7 +1482,7 @@ __device__ __forceinline__ void merge_elems(const Tree& tree, int e0, int total,
 #pragma unroll
     for (int t = 0; t < W; ++t) {
       const int tt = t < gsize ? t : 0;
-      ls[q][t] = load_partial1(lp + tt * lse_step);
+      ls[q][t] = load_partial1(tree.part_lse, lp + tt * lse_step);
       vs[q][t] = load_partial4(tree.part_o, op + tt * o_step);
     }
   }
