@@ -1459,11 +1459,21 @@ __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected
 // merge_elems handles E four-dim elements e0, e0 + 64*NW, ... (< total) of the group's rows: it
 // issues the loads of all items for all of them at once (unconditional: slots past the group
 // re-read its first item and are masked by their lse, elements past the rows re-read e0's), so
-// the step is one memory round trip.
+// the step is one memory round trip.  A row's D/4 elements sit on D/4 consecutive lanes of one
+// wave; when the group has at most that many items, lane j of the row loads item j's
+// log-sum-exp and the row's lanes exchange them (ds_bpermute) instead of each loading all W:
+// W loads per element fewer in flight, which keeps W = 32 items (64 loads per thread otherwise,
+// past the 63 the memory counter tracks) to one round trip.
 template <int D, int NW, int W, int E, class Tree>
 __device__ __forceinline__ void merge_elems(const Tree& tree, int e0, int total, int gslot,
                                             int stride, int gsize, bool final, float* s_lse) {
+  constexpr int kRowLanes = D / 4;
+  constexpr bool kLaneLse = W <= kRowLanes;
+  static_assert((64 * NW) % kRowLanes == 0 && kRowLanes <= 64, "a row's lanes in one wave");
+  const int lane = e0 & 63;
+  const int row_lane0 = lane & ~(kRowLanes - 1);  // first lane of this lane's row group
   float ls[E][W];
+  float lsl[E];  // kLaneLse: item (lane - row_lane0)'s log-sum-exp of element q's row
   f32x4 vs[E][W];
   int hh[E], d[E];
   // Item t of the group sits t * stride slots after the first: the row's addresses are formed
@@ -1479,12 +1489,24 @@ __device__ __forceinline__ void merge_elems(const Tree& tree, int e0, int total,
     d[q] = 4 * (ee - hh[q] * (D / 4));
     const float* lp = tree.lse(hh[q], gslot);
     const float* op = tree.o(hh[q], gslot) + d[q];
+    if constexpr (kLaneLse) {
+      const int j = lane - row_lane0;  // = d[q] / 4
+      lsl[q] = load_partial1(tree.part_lse, lp + (j < gsize ? j : 0) * lse_step);
+    }
 #pragma unroll
     for (int t = 0; t < W; ++t) {
       const int tt = t < gsize ? t : 0;
-      ls[q][t] = load_partial1(tree.part_lse, lp + tt * lse_step);
+      if constexpr (!kLaneLse) ls[q][t] = load_partial1(tree.part_lse, lp + tt * lse_step);
       vs[q][t] = load_partial4(tree.part_o, op + tt * o_step);
     }
+  }
+  if constexpr (kLaneLse) {
+    // (Every lane of a row group runs this: total is a multiple of the row's lanes, and lanes
+    // past it hold e0's row, the same for the whole group.)
+#pragma unroll
+    for (int q = 0; q < E; ++q)
+#pragma unroll
+      for (int t = 0; t < W; ++t) ls[q][t] = __shfl(lsl[q], row_lane0 + t);
   }
 #pragma unroll
   for (int q = 0; q < E; ++q) {
