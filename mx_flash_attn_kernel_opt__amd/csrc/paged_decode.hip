@@ -1456,6 +1456,32 @@ __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected
 // merged rows go to the output (`final`) or to the group's first slot (lse to s_lse, which the
 // caller stores after a barrier).
 //
+// The arithmetic of one element's merge over items t < gsize of W (items past gsize weigh 0):
+// returns the merged dims and sets lse.
+template <int W>
+__device__ __forceinline__ f32x4 lse_merge(float (&ls)[W], const f32x4 (&vs)[W], int gsize,
+                                           float& lse) {
+  float mx = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < W; ++t) {
+    if (t >= gsize) ls[t] = -INFINITY;
+    mx = fmaxf(mx, ls[t]);
+  }
+  const bool seen = mx > -INFINITY;
+  const float mref = seen ? mx : 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float wsum = 0.f;
+#pragma unroll
+  for (int t = 0; t < W; ++t) {
+    const float w = __builtin_amdgcn_exp2f(ls[t] - mref);  // 0 for t >= gsize
+    wsum += w;
+    acc += w * vs[t];
+  }
+  acc *= seen ? 1.0f / wsum : 0.f;
+  lse = seen ? mx + log2f(wsum) : -INFINITY;
+  return acc;
+}
+
 // merge_elems handles E four-dim elements e0, e0 + 64*NW, ... (< total) of the group's rows: it
 // issues the loads of all items for all of them at once (unconditional: slots past the group
 // re-read its first item and are masked by their lse, elements past the rows re-read e0's), so
@@ -1511,24 +1537,8 @@ __device__ __forceinline__ void merge_elems(const Tree& tree, int e0, int total,
 #pragma unroll
   for (int q = 0; q < E; ++q) {
     if (e0 + q * 64 * NW >= total) break;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int t = 0; t < W; ++t) {
-      if (t >= gsize) ls[q][t] = -INFINITY;
-      mx = fmaxf(mx, ls[q][t]);
-    }
-    const bool seen = mx > -INFINITY;
-    const float mref = seen ? mx : 0.f;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    float wsum = 0.f;
-#pragma unroll
-    for (int t = 0; t < W; ++t) {
-      const float w = __builtin_amdgcn_exp2f(ls[q][t] - mref);  // 0 for t >= gsize
-      wsum += w;
-      acc += w * vs[q][t];
-    }
-    acc *= seen ? 1.0f / wsum : 0.f;
-    const float lse = seen ? mx + log2f(wsum) : -INFINITY;
+    float lse;
+    const f32x4 acc = lse_merge<W>(ls[q], vs[q], gsize, lse);
     if (final) {
       tree.store(hh[q], d[q], acc, lse);
     } else {
@@ -1863,6 +1873,54 @@ struct BalancedTree {
   }
 };
 
+// A unit cut into exactly two pieces, merged by the workgroup of its first piece without storing
+// that piece: the first piece is the last of its workgroup's share (the unit starts inside the
+// share and runs past its end) and the second the first of the next workgroup's, which has
+// almost always stored its partial and arrived by then.  Thread 0 reads the unit's level-0
+// counter (relaxed, agent scope, like the increments of arrive_last): when it reads 1, the
+// second piece's stores were complete before its increment, so this workgroup resets the
+// counter, loads that partial (sc1, after the barrier that hands the read to every thread) and
+// writes the output with the same arithmetic as a merge step of two items (lse_merge).  Returns
+// false, having changed nothing, when the second piece has not arrived: the caller then stores
+// this piece and arrives as usual.  `own(hh, d, lse)` gives this piece's merged dims of row hh.
+template <int D, int NW, int KT, class Own>
+__device__ __forceinline__ bool merge_first_of_two(const BalancedTree<D>& tree, int nrows,
+                                                   const Own& own, int* s_flag) {
+  if (threadIdx.x == 0) {
+    uint32_t* c = tree.counter(0, 0);
+    const bool ready = __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1u;
+    if (ready) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_flag = ready ? 1 : 0;
+  }
+  __syncthreads();
+  if (*s_flag == 0) return false;
+  constexpr int kE = (16 * KT * (D / 4) + 64 * NW - 1) / (64 * NW);  // elements per thread
+  const int total = nrows * (D / 4);
+  const int tid = threadIdx.x;
+  float ls[kE][2];
+  f32x4 vs[kE][2];
+#pragma unroll
+  for (int q = 0; q < kE; ++q) {  // the second piece's loads first, all in one round
+    const int e = min(tid + q * 64 * NW, total - 1);
+    const int hh = e / (D / 4);
+    const int d = 4 * (e - hh * (D / 4));
+    ls[q][1] = load_partial1(tree.part_lse, tree.lse(hh, 1));
+    vs[q][1] = load_partial4(tree.part_o, tree.o(hh, 1) + d);
+  }
+#pragma unroll
+  for (int q = 0; q < kE; ++q) {
+    const int e = tid + q * 64 * NW;
+    if (e >= total) break;
+    const int hh = e / (D / 4);
+    const int d = 4 * (e - hh * (D / 4));
+    vs[q][0] = own(hh, d, ls[q][0]);
+    float lse;
+    const f32x4 acc = lse_merge<2>(ls[q], vs[q], 2, lse);
+    tree.store(hh, d, acc, lse);
+  }
+  return true;
+}
+
 // One launch of num_groups workgroups covers the whole batch whatever the length mix.  Every
 // (sequence b, KV head and row group j) "unit" with n_b = ceil(L_b/16) > 0 chunks occupies n_b +
 // unit_overhead consecutive positions of one global line (units in (b, j) order; the
@@ -2119,24 +2177,27 @@ void mx_paged_decode_balanced(
         // Piece k of the unit goes to slot slot0 + k and is level-0 item k of its merge tree.
         const int slot0 = first_wg + unit;
         const int item = wg - first_wg;
-        {
+        const BalancedTree<D> tree{sh, part_o, part_lse, counters, out, rbase, kv, r0, slot0, TR};
+        auto own = [&](int hh, int d, float& lse) -> f32x4 {
+          if constexpr (kPairW)
+            return merged_head_pair<D>(lds, hh, d, lse, sh);
+          else
+            return merged_head<D, NW, KT>(lds, hh, d, lse);
+        };
+        if (!(npieces == 2 && item == 0 &&
+              merge_first_of_two<D, NW, KT>(tree, nrows, own, &s_int[NW + 2]))) {
           float* po = part_o + (int64_t)(slot0 + item) * TR * D;
           float* pl = part_lse + (int64_t)(slot0 + item) * TR;
           for (int e = tid; e < nrows * (D / 4); e += 64 * NW) {
             const int hh = e / (D / 4);
             const int d = 4 * (e - hh * (D / 4));
             float lse;
-            f32x4 o;
-            if constexpr (kPairW)
-              o = merged_head_pair<D>(lds, hh, d, lse, sh);
-            else
-              o = merged_head<D, NW, KT>(lds, hh, d, lse);
+            const f32x4 o = own(hh, d, lse);
             store_partial4(part_o, po + hh * D + d, o);
             if (d == 0) store_partial1(pl + hh, lse);
           }
+          merge_tree<D, NW, kMergeFanIn>(tree, item, npieces, nrows, s_lse, &s_int[NW + 2]);
         }
-        const BalancedTree<D> tree{sh, part_o, part_lse, counters, out, rbase, kv, r0, slot0, TR};
-        merge_tree<D, NW, kMergeFanIn>(tree, item, npieces, nrows, s_lse, &s_int[NW + 2]);
       }
       // The merged states in LDS share bytes with the K tiles the next piece streams into:
       // no wave may start that piece until every wave has finished reading them.

@@ -10,7 +10,10 @@ the invariants the device code relies on:
     count, and its pieces are items 0 .. n-1, each held once;
   * slots stay below groups + units and are disjoint between units;
   * a merge never reads an item that has not been written, each unit gets exactly one final
-    write, and every counter is back at zero when the launch ends.
+    write, and every counter is back at zero when the launch ends;
+  * a unit cut in two is merged by its first piece's workgroup without storing that piece
+    (merge_first_of_two) only once the second piece has been written and counted, and
+    otherwise through the tree as before.
 Line constants as in the kernel: 8 positions per chunk (16 for a pair of KV heads) and 64 per
 unit; the uniform-batch rule; shares of at least one chunk's weight.
 """
@@ -54,9 +57,12 @@ def _tree(counters, written, finals, unit, slot0, item, nitems, rng_yield):
     raise AssertionError("merge tree deeper than its levels")
 
 
-def balanced_launch(lens, ups, groups, chunk_weight=8, unit_overhead=64, seed=0):
+def balanced_launch(lens, ups, groups, chunk_weight=8, unit_overhead=64, seed=0,
+                    first_of_two="checked"):
     """Runs one launch of the balanced schedule's control logic; returns (chunks covered per
-    unit, final writes per unit, slots used)."""
+    unit, final writes per unit, slots used).  first_of_two: "checked" (the kernel), "off" (no
+    direct merge of units cut in two) or "unchecked" (a planted mistake: the first piece merges
+    without reading the counter)."""
     B = len(lens)
     rng = random.Random(seed)
     n = [(x + CHUNK - 1) // CHUNK if x > 0 else 0 for x in lens]
@@ -114,9 +120,20 @@ def balanced_launch(lens, ups, groups, chunk_weight=8, unit_overhead=64, seed=0)
                     assert 0 <= item < npieces
                     assert slot0 + item < groups + units
                     slots_of.setdefault(unit, set()).add(slot0 + item)
-                    written[(0, slot0 + item)] = True
-                    yield from _tree(counters, written, finals, unit, slot0, item, npieces,
-                                     rng)
+                    direct = False
+                    if npieces == 2 and item == 0 and first_of_two != "off":
+                        yield  # thread 0 reads the unit's level-0 counter
+                        if first_of_two == "unchecked" or counters[0].get(slot0, 0) == 1:
+                            assert written.get((0, slot0 + 1)), \
+                                f"direct merge of unit {unit} reads an unwritten second piece"
+                            counters[0][slot0] = 0
+                            assert unit not in finals
+                            finals[unit] = "first of two"
+                            direct = True
+                    if not direct:
+                        written[(0, slot0 + item)] = True
+                        yield from _tree(counters, written, finals, unit, slot0, item, npieces,
+                                         rng)
             u0 += span
             if u0 >= x_end:
                 break
@@ -142,6 +159,11 @@ def balanced_launch(lens, ups, groups, chunk_weight=8, unit_overhead=64, seed=0)
 
 def _check_balanced(lens, ups, groups, chunk_weight=8, seed=0):
     covered, finals, slots_of = balanced_launch(lens, ups, groups, chunk_weight, seed=seed)
+    _check_units(lens, ups, covered, finals, slots_of)
+    return finals
+
+
+def _check_units(lens, ups, covered, finals, slots_of):
     n = [(x + CHUNK - 1) // CHUNK if x > 0 else 0 for x in lens]
     for b, nb in enumerate(n):
         for j in range(ups):
@@ -158,7 +180,8 @@ def _check_balanced(lens, ups, groups, chunk_weight=8, seed=0):
             assert len(first) == 1 and counts == {len(pieces)}, (unit, pieces)
             items = sorted(p[2] - p[3] for p in pieces)
             assert items == list(range(len(pieces)))
-            assert finals[unit] == ("direct" if len(pieces) == 1 else "merged")
+            expect = {1: {"direct"}, 2: {"merged", "first of two"}}.get(len(pieces), {"merged"})
+            assert finals[unit] in expect, (unit, len(pieces), finals[unit])
     all_slots = [s for v in slots_of.values() for s in v]
     assert len(all_slots) == len(set(all_slots)), "slots shared between units"
 
@@ -193,7 +216,31 @@ def test_ragged_config_shape():
     r = random.Random(4)
     lens = [r.randint(1, 15) if r.random() < 0.1 else int(math.exp(r.uniform(0, math.log(8192))))
             for _ in range(256)]
-    _check_balanced(lens, 4, 256)
+    finals = _check_balanced(lens, 4, 256)
+    # Units cut in two are common here, and the interleaving lets some be merged directly.
+    assert list(finals.values()).count("first of two") > 0
+
+
+def test_first_of_two_without_the_counter_read_is_caught():
+    """A planted mistake: the first piece of a unit cut in two merging without reading the
+    counter reads an unwritten second piece under some interleaving (or, when the second piece
+    was written but not yet counted, leaves its counter non-zero)."""
+    r = random.Random(4)
+    lens = [r.randint(1, 15) if r.random() < 0.1 else int(math.exp(r.uniform(0, math.log(8192))))
+            for _ in range(256)]
+    caught = 0
+    for seed in range(20):
+        try:
+            balanced_launch(lens, 4, 256, seed=seed, first_of_two="unchecked")
+        except AssertionError as e:
+            assert "unwritten second piece" in str(e) or "counters left non-zero" in str(e)
+            caught += 1
+    assert caught > 0
+    # and the checked form agrees with the plain tree on every interleaving tried
+    for seed in range(20):
+        _, finals_off, _ = balanced_launch(lens, 4, 256, seed=seed, first_of_two="off")
+        _, finals_on, _ = balanced_launch(lens, 4, 256, seed=seed)
+        assert set(finals_off) == set(finals_on)
 
 
 @pytest.mark.parametrize("splits", [2, 7, 8, 9, 64, 65, 511, 4096])
