@@ -2184,8 +2184,13 @@ void mx_paged_decode_balanced(
           else
             return merged_head<D, NW, KT>(lds, hh, d, lse);
         };
-        if (!(npieces == 2 && item == 0 &&
-              merge_first_of_two<D, NW, KT>(tree, nrows, own, &s_int[NW + 2]))) {
+        // (Not at head_dim 256: there its registers spilled in the causal kernel.)
+        bool merged = false;
+        if constexpr (D <= 128) {
+          if (npieces == 2 && item == 0)
+            merged = merge_first_of_two<D, NW, KT>(tree, nrows, own, &s_int[NW + 2]);
+        }
+        if (!merged) {
           float* po = part_o + (int64_t)(slot0 + item) * TR * D;
           float* pl = part_lse + (int64_t)(slot0 + item) * TR;
           for (int e = tid; e < nrows * (D / 4); e += 64 * NW) {
