@@ -317,6 +317,24 @@ def test_balanced_repeated_calls_are_identical():
     assert read_device_status(ws) == 0
 
 
+@pytest.mark.parametrize("B,Hkv,L", [(1, 1, 5000), (8, 4, 3000), (16, 4, 2048)])
+def test_units_cut_in_two_merge_identically(B, Hkv, L):
+    """Uniform lengths with two workgroups per unit cut every unit into two equal pieces that
+    end together.  The first piece's workgroup merges the unit itself when the second piece has
+    already arrived, and otherwise stores its piece and arrives like any other cut unit; which
+    of the two happens depends on timing, and both must give the same bits.  Twenty calls are
+    compared bitwise, and the first with the oracle."""
+    units = B * Hkv
+    spec = W.custom_spec(f"cut2_b{B}_hkv{Hkv}", [L] * B, 4 * Hkv, Hkv, 128, 16)
+    inp = W.make_inputs(spec, seed=B + Hkv, device=DEV)
+    ws = torch.zeros(1 << 24, dtype=torch.uint8, device=DEV)
+    outs = [_decode(inp, num_splits=-2 * units, workspace=ws).clone() for _ in range(20)]
+    for i, o in enumerate(outs[1:], 1):
+        assert torch.equal(o, outs[0]), f"call {i} differs from call 0"
+    _check(inp, outs[0], label=f"units cut in two B={B} Hkv={Hkv}")
+    assert read_device_status(ws) == 0
+
+
 @pytest.mark.parametrize("name,ns", [("ragged", 0), ("long_b1_32k", 0), ("long_b4_32k", 0)])
 def test_merge_trees_are_placement_independent(name, ns):
     """The first workgroup of a launch lands on whichever XCD the hardware queue's rotation
